@@ -1,0 +1,108 @@
+/*
+ * fm_layer_forward.c -- MoE layer driver (host C) over the C-ABI launchers.
+ *
+ * Decode mirrors moe_forward (layer_forward.h:1071-1322) and the GPU CMD2/CMD3
+ * sequence of fused_layer_forward (layer_forward.h:3506-3993); prefill mirrors
+ * pfb_batched_shared_expert + the per-token routed loop (batched_prefill.h:
+ * 122-308), with routed experts run as one grouped GEMM instead of per token.
+ * No host synchronisation: routing results stay on the device.
+ */
+#include "fm_layer_forward.h"
+
+#include <stdint.h>
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int layer_ok(const fm_moe_layer *L, int K) {
+    return L && L->router_w && L->router_s && L->router_b && L->pool.num_experts > 0 && K >= 1 &&
+           K <= FM_MAX_K && (!L->has_shared || (L->seg_w && L->seg_s && L->seg_b));
+}
+
+size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K) {
+    if (!L) return 0;
+    size_t n = align256((size_t)L->pool.num_experts * sizeof(float)); /* logits */
+    n += align256(sizeof(float));                                      /* seg score */
+    n += align256((size_t)K * sizeof(int));                            /* idx */
+    n += align256((size_t)K * sizeof(float));                          /* weights */
+    n += fm_moe_decode_workspace_size(K + 1, L->pool.hidden, L->pool.inter);
+    return n;
+}
+
+int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
+    if (!layer_ok(L, K) || !h_post || !out) return FM_ERR_INVALID;
+    size_t need = fm_moe_forward_workspace_size(L, K);
+    if (!ws || ws_bytes < need) return FM_ERR_WORKSPACE;
+    char *p = (char *)ws;
+    float *logits = (float *)p;
+    p += align256((size_t)L->pool.num_experts * sizeof(float));
+    float *seg = (float *)p;
+    p += align256(sizeof(float));
+    int *idx = (int *)p;
+    p += align256((size_t)K * sizeof(int));
+    float *w = (float *)p;
+    p += align256((size_t)K * sizeof(float));
+    size_t rest = ws_bytes - (size_t)(p - (char *)ws);
+
+    /* CMD2: routing gate (+ shared_expert_gate) share h_post (3506-3512) */
+    fm_batch_matvec_spec specs[2] = {
+        {L->router_w, L->router_s, L->router_b, logits, L->pool.num_experts, L->pool.hidden,
+         L->pool.group_size, L->router_bits},
+        {L->seg_w, L->seg_s, L->seg_b, seg, 1, L->pool.hidden, L->pool.group_size, L->seg_bits},
+    };
+    int rc = fm_batch_matvec(h_post, L->pool.hidden, specs, L->has_shared ? 2 : 1, stream);
+    if (rc) return rc;
+    /* softmax -> top-K -> renormalise (3519-3523) */
+    rc = fm_route_topk(logits, 1, (int)L->pool.num_experts, K, idx, w, stream);
+    if (rc) return rc;
+    /* CMD3: experts + shared expert + combine (3895-3993) */
+    return fm_moe_decode_pool(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL,
+                              L->shared_bits, L->has_shared ? seg : NULL, h_post, h_mid, out,
+                              out_bf16, p, rest, stream);
+}
+
+size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
+    if (!L || T <= 0) return 0;
+    size_t n = align256((size_t)T * L->pool.num_experts * sizeof(float)); /* logits */
+    n += align256((size_t)T * sizeof(float));                             /* seg scores */
+    n += align256((size_t)T * K * sizeof(int));
+    n += align256((size_t)T * K * sizeof(float));
+    size_t g1 = fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden);
+    size_t g2 = fm_prefill_moe_workspace_size(T, K, &L->pool);
+    return n + (g1 > g2 ? g1 : g2);
+}
+
+int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
+                           const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
+                           size_t ws_bytes, void *stream) {
+    if (!layer_ok(L, K) || T <= 0 || !h_post || !out) return FM_ERR_INVALID;
+    size_t need = fm_moe_prefill_workspace_size(L, K, T);
+    if (!ws || ws_bytes < need) return FM_ERR_WORKSPACE;
+    char *p = (char *)ws;
+    float *logits = (float *)p;
+    p += align256((size_t)T * L->pool.num_experts * sizeof(float));
+    float *seg = (float *)p;
+    p += align256((size_t)T * sizeof(float));
+    int *idx = (int *)p;
+    p += align256((size_t)T * K * sizeof(int));
+    float *w = (float *)p;
+    p += align256((size_t)T * K * sizeof(float));
+    size_t rest = ws_bytes - (size_t)(p - (char *)ws);
+
+    /* routing gate and shared_expert_gate over all tokens (batched_prefill.h:164-182) */
+    int rc = fm_pfb_gemm(L->router_w, L->router_s, L->router_b, h_post, logits, (uint32_t)T,
+                         L->pool.num_experts, L->pool.hidden, L->pool.group_size, L->router_bits,
+                         p, rest, stream);
+    if (rc) return rc;
+    if (L->has_shared) {
+        rc = fm_pfb_gemm(L->seg_w, L->seg_s, L->seg_b, h_post, seg, (uint32_t)T, 1, L->pool.hidden,
+                         L->pool.group_size, L->seg_bits, p, rest, stream);
+        if (rc) return rc;
+    }
+    /* per-token softmax / top-K / renormalise (batched_prefill.h:256-261) */
+    rc = fm_route_topk(logits, T, (int)L->pool.num_experts, K, idx, w, stream);
+    if (rc) return rc;
+    return fm_prefill_moe(&L->pool, T, K, idx, w, L->has_shared ? &L->shared : NULL,
+                          L->shared_bits, L->has_shared ? seg : NULL, h_post, h_mid, out,
+                          out_bf16, p, rest, stream);
+}

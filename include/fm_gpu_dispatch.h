@@ -1,0 +1,218 @@
+/*
+ * fm_gpu_dispatch.h -- C ABI of the MI355X (gfx950) quantized-expert backend.
+ *
+ * This is the drop-in boundary for Flash-MoE's quantized-expert hot path: the
+ * launchers below replace the Metal encode/dispatch functions of
+ * metal_infer/gpu_dispatch.h and metal_infer/metal_ctx.h (cited per entry
+ * point) with plain extern "C" calls on a HIP stream.
+ *
+ * Conventions (all entry points):
+ *   - Pointers named W/scales/biases/x/out/... are DEVICE pointers; arrays
+ *     documented as "host" are read on the host during the call only.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     Launches are asynchronous; nothing is synchronised unless stated.
+ *   - Return 0 on success or a negative FM_ERR_* code; fm_last_error() then
+ *     holds a message (thread-local).  The reference's void functions only
+ *     print; these report instead.
+ *   - Quantisation format (shaders.metal:13-25): W is uint32 [out, in*bits/32],
+ *     codes LSB-first ((w >> bits*n) & mask is element (32/bits)*col + n);
+ *     scales/biases are bf16 [out, in/group_size]; w = code*scale + bias.
+ *     bits in {2, 4}; group_size 64 (the only size Flash-MoE models use).
+ *   - Nothing allocates device memory on the hot path: the decode/prefill
+ *     launchers take a caller workspace sized by the *_workspace_size query.
+ *   - Calls are thread-compatible: concurrent callers use distinct streams
+ *     and distinct workspaces.
+ */
+#ifndef FM_GPU_DISPATCH_H
+#define FM_GPU_DISPATCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FM_OK 0
+#define FM_ERR_INVALID (-1)     /* bad argument: null pointer, dims, bits, K */
+#define FM_ERR_WORKSPACE (-2)   /* caller workspace smaller than required    */
+#define FM_ERR_HIP (-3)         /* a HIP runtime call or launch failed        */
+#define FM_ERR_UNSUPPORTED (-4) /* shape outside what the kernels implement   */
+
+#define FM_MAX_K 16 /* routed experts per token (metal_ctx.h:76 MAX_K) */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *fm_last_error(void);
+
+/* Library version string. */
+const char *fm_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Expert blob layout: config.h:94-137 compute_expert_offsets().             */
+/* ------------------------------------------------------------------------ */
+
+/* Byte offsets of the 9 tensors of one packed expert (layer_XX.bin entry):
+ * off[0..8] = gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s,
+ * down_b; size = bytes per expert (7,077,888 for 4-bit 4096/1024/64,
+ * 3,932,160 for 2-bit). */
+typedef struct {
+    size_t off[9];
+    size_t size;
+} fm_expert_layout;
+
+int fm_expert_layout_compute(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                             int bits, fm_expert_layout *out);
+
+/* Device pointers to one expert's nine tensors.  Routed experts come from a
+ * blob (fm_expert_from_blob); the shared expert's tensors live separately in
+ * the weight file (layer_forward.h:3506-3512, 3906-3937). */
+typedef struct {
+    const void *gate_w, *gate_s, *gate_b;
+    const void *up_w, *up_s, *up_b;
+    const void *down_w, *down_s, *down_b;
+} fm_expert_weights;
+
+int fm_expert_from_blob(const void *blob, const fm_expert_layout *layout,
+                        fm_expert_weights *out);
+
+/* A device-resident pool of experts (one MoE layer): blobs[e] is the device
+ * address of expert e's packed blob, bits[e] its width (2 or 4) -- the HBM
+ * counterpart of TieredExpertInfo (config.h:81-92) and expert_offset_size()
+ * (timing.h:138-148).  Both arrays live in device memory. */
+typedef struct {
+    const void *const *blobs; /* device [num_experts] */
+    const uint8_t *bits;      /* device [num_experts] */
+    uint32_t num_experts;
+    uint32_t hidden, inter, group_size;
+} fm_expert_pool;
+
+/* ------------------------------------------------------------------------ */
+/* Dequant matvec                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* out[out_dim] = dequant(W) x.  Replaces fast_dequant_matvec (metal_ctx.h:
+ * 907-929) and gpu_encode_dequant_matvec_with_io_bufs (gpu_dispatch.h:
+ * 162-206); `bits` selects dequant_matvec_4bit_v3 (shaders.metal:266-359) or
+ * dequant_matvec_2bit (shaders.metal:447-537) semantics.  in_dim must be a
+ * multiple of group_size and at most 16384. */
+int fm_dequant_matvec(const void *W, const void *scales, const void *biases,
+                      const float *x, float *out, uint32_t out_dim, uint32_t in_dim,
+                      uint32_t group_size, int bits, void *stream);
+
+/* gpu_dispatch.h:10-19 BatchMatvecSpec, with a device output pointer in place
+ * of out_cpu/batch_slot and a per-spec bit width. */
+typedef struct {
+    const void *W, *scales, *biases;
+    float *out;
+    uint32_t out_dim, in_dim, group_size;
+    int bits;
+} fm_batch_matvec_spec;
+
+/* N matvecs sharing one input x, in ONE kernel launch.  Replaces
+ * gpu_batch_matvec / gpu_encode_batch_matvec / fast_batch_matvec
+ * (gpu_dispatch.h:23-147, 729-742).  specs is a host array, num_specs <= 64;
+ * every spec's in_dim must equal x_dim. */
+int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *specs,
+                    int num_specs, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Decode: K routed experts + shared expert, SwiGLU, weighted combine        */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace bytes for fm_moe_decode / fm_moe_decode_pool /
+ * fm_encode_experts_batched with n_slots = K (+1 if a shared expert). */
+size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
+
+/* K expert FFNs sharing input x, one output per expert:
+ *   expert_out[k] = down(silu(gate x) * up x)            [K][hidden] fp32
+ * Replaces gpu_encode_experts_batched (gpu_dispatch.h:461-609): experts/bits
+ * (and valid, may be NULL) are host arrays [K]; an expert with valid[k]==0 is
+ * skipped and its output row left untouched, as in gpu_dispatch.h:485. */
+int fm_encode_experts_batched(int K, const int *valid, const fm_expert_weights *experts,
+                              const int *bits, uint32_t hidden, uint32_t inter,
+                              uint32_t group_size, const float *x, float *expert_out,
+                              void *ws, size_t ws_bytes, void *stream);
+
+/* Weighted combine (moe_combine_residual, shaders.metal:1865-1900, with the
+ * CPU semantics of layer_forward.h:1257,1295-1305 and no K<=8 limit):
+ *   out[i] = h_mid[i] + sum_k w[k]*expert_outs[k][i] + sigmoid(g)*shared_out[i]
+ * weights: device [K]; valid: device [K] or NULL; h_mid, shared_out,
+ * shared_gate_score (device scalar g) may be NULL (terms dropped); out_bf16
+ * (device, may be NULL) receives the round-to-nearest-even bf16 of out. */
+int fm_moe_combine(const float *h_mid, const float *expert_outs, const float *weights,
+                   const int *valid, int K, const float *shared_out,
+                   const float *shared_gate_score, float *out, uint16_t *out_bf16,
+                   uint32_t dim, void *stream);
+
+/* The fused decode step (CMD3 of layer_forward.h:3895-3993): K routed experts
+ * and the shared expert, gate/up/SwiGLU/down, weighted accumulation and the
+ * residual, in two kernel launches.
+ *   out = h_mid + sum_k weights[k]*E_k(x) + sigmoid(shared_gate_score)*S(x)
+ * experts/bits/weights/valid are HOST arrays [K] (K <= FM_MAX_K, routing done
+ * on the CPU as in layer_forward.h:3519-3523); valid may be NULL.  shared may
+ * be NULL (no shared term).  h_mid and out_bf16 may be NULL. */
+int fm_moe_decode(int K, const fm_expert_weights *experts, const int *bits,
+                  const float *weights, const int *valid,
+                  const fm_expert_weights *shared, int shared_bits,
+                  float shared_gate_score, uint32_t hidden, uint32_t inter,
+                  uint32_t group_size, const float *x, const float *h_mid,
+                  float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
+                  void *stream);
+
+/* Same step with routing on the device: idx/weights are DEVICE arrays [K]
+ * (e.g. from fm_route_topk), experts come from `pool`, shared_gate_score is a
+ * device scalar (may be NULL: weight 1 for the shared expert is NOT implied;
+ * NULL drops the sigmoid and uses weight 1.0f).  No host synchronisation. */
+int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
+                       const float *weights, const fm_expert_weights *shared,
+                       int shared_bits, const float *shared_gate_score,
+                       const float *x, const float *h_mid, float *out,
+                       uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Routing                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* For each of T tokens: softmax over E logits, top-K in the slot order of
+ * cpu_topk, renormalised weights -- cpu_softmax / cpu_topk /
+ * cpu_normalize_weights (cpu_kernels.h:263-309) as called at
+ * layer_forward.h:3519-3523 and batched_prefill.h:256-261.
+ * logits [T,E], idx [T,K] int32, weights [T,K] fp32; E <= 4096, K <= 64. */
+int fm_route_topk(const float *logits, int T, int E, int K, int *idx, float *weights,
+                  void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Prefill                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace bytes for fm_prefill_moe with T tokens, K routed per token. */
+size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool);
+
+/* Batched-prefill MoE layer as a per-expert grouped dequant-GEMM on MFMA.
+ * Same result as the per-token loop of batched_prefill.h:241-308 plus the
+ * shared expert of pfb_batched_shared_expert (batched_prefill.h:122-226):
+ *   out[t] = h_mid[t] + sum_k w[t,k] E_{idx[t,k]}(X[t]) + sigmoid(g[t]) S(X[t])
+ * idx/weights: device [T,K]; X, h_mid, out: device [T,hidden] fp32; X values
+ * must be bf16-representable (hidden states arrive as bf16); shared,
+ * shared_gate_scores (device [T]), h_mid and out_bf16 may be NULL. */
+int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const int *idx,
+                   const float *weights, const fm_expert_weights *shared, int shared_bits,
+                   const float *shared_gate_scores, const float *X, const float *h_mid,
+                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
+                   void *stream);
+
+/* Workspace bytes for fm_pfb_gemm. */
+size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim);
+
+/* Y[N,out_dim] = X[N,in_dim] dequant(W)^T on MFMA.  Replaces pfb_encode_gemm
+ * (batched_prefill.h:30-67) / dequant_gemm_4bit_batch (shaders.metal:
+ * 2140-2216) without the N <= 32 limit.  X is fp32 of any value (split into
+ * two bf16 terms internally). */
+int fm_pfb_gemm(const void *W, const void *scales, const void *biases, const float *X,
+                float *Y, uint32_t N, uint32_t out_dim, uint32_t in_dim,
+                uint32_t group_size, int bits, void *ws, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FM_GPU_DISPATCH_H */

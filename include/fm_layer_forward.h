@@ -1,0 +1,54 @@
+/*
+ * fm_layer_forward.h -- host-side MoE layer driver over the gfx950 backend.
+ *
+ * C counterpart of the MoE half of the reference's layer forward: the
+ * routing-gate + shared-expert-gate matvecs, softmax/top-K, K routed experts
+ * + the shared expert, and the combine into the residual stream.  Everything
+ * stays on the device; the calls only enqueue work on `stream`.
+ */
+#ifndef FM_LAYER_FORWARD_H
+#define FM_LAYER_FORWARD_H
+
+#include "fm_gpu_dispatch.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One MoE layer's device-resident weights (model.layers.N.mlp.*). */
+typedef struct {
+    const void *router_w, *router_s, *router_b; /* mlp.gate [num_experts, hidden]       */
+    int router_bits;
+    const void *seg_w, *seg_s, *seg_b;          /* mlp.shared_expert_gate [1, hidden]   */
+    int seg_bits;
+    fm_expert_weights shared;                   /* mlp.shared_expert.{gate,up,down}_proj */
+    int shared_bits;
+    int has_shared;
+    fm_expert_pool pool;                        /* routed experts (packed blobs)         */
+} fm_moe_layer;
+
+size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K);
+
+/* Decode step for one token: moe_forward (layer_forward.h:1071-1322) with the
+ * GPU dispatch of fused_layer_forward (layer_forward.h:3506-3993):
+ *   logits = router(h_post); g = seg(h_post)                  (3506-3512)
+ *   idx, w = topK(softmax(logits)), renormalised               (3519-3523)
+ *   out = h_mid + sum_k w_k E_idx[k](h_post) + sigmoid(g) S(h_post)
+ * h_post, h_mid, out: device [hidden] fp32; out_bf16 optional. */
+int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
+
+size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T);
+
+/* Prefill of T tokens: the MoE part of batched_prefill (batched_prefill.h:
+ * 122-308) -- router and shared-expert-gate GEMMs over all tokens, per-token
+ * routing, then the grouped expert GEMM (routed + shared) and the combine.
+ * h_post, h_mid, out: device [T, hidden] fp32, h_post bf16-representable. */
+int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
+                           const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
+                           size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FM_LAYER_FORWARD_H */

@@ -1,0 +1,226 @@
+"""GPU parity of the decode path through the libfmoe C ABI against the oracle.
+
+Bars: routing indices bit-exact; fp32 outputs norm_err <= 1e-3; bf16 outputs
+norm_err <= 2e-2 (norm_err = max|g - r| / max|r|, see helpers.py).
+"""
+import numpy as np
+import pytest
+
+import fmoe_amd as fm
+from fmoe_amd import synth
+from helpers import GS, HIDDEN, INTER, TOL_BF16, TOL_F32, bf16_out, experts, matrix, norm_err
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.mark.parametrize("bits,out_dim,in_dim", [
+    (4, 4096, 4096), (4, 1024, 4096), (4, 4096, 1024), (4, 1000, 2048), (4, 7, 512), (4, 300, 8192),
+    (4, 33, 3072), (2, 4096, 4096), (2, 4096, 1024), (2, 129, 8192), (4, 64, 16384)])
+def test_matvec(orc, dev, bits, out_dim, in_dim):
+    import torch
+    say("matvec", bits, out_dim, in_dim)
+    W, s, b = matrix(out_dim * 7 + in_dim, out_dim, in_dim, bits)
+    x = synth.hidden_vec(synth.rng_for(3, in_dim), in_dim)
+    out = torch.empty(out_dim, dtype=torch.float32, device=dev)
+    fm.dequant_matvec(T(W, dev), T(s, dev), T(b, dev), T(x, dev), out, bits)
+    torch.cuda.synchronize()
+    ref = orc.matvec(bits, W, s, b, x)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_batch_matvec_mixed(orc, dev):
+    import torch
+    say("batch_matvec")
+    x = synth.hidden_vec(synth.rng_for(4), HIDDEN)
+    specs, refs = [], []
+    for i, (rows, bits) in enumerate([(512, 4), (1024, 4), (1024, 2), (1, 4), (77, 2)]):
+        W, s, b = matrix(50 + i, rows, HIDDEN, bits)
+        out = torch.full((rows,), float("nan"), dtype=torch.float32, device=dev)
+        specs.append((T(W, dev), T(s, dev), T(b, dev), out, bits))
+        refs.append(orc.matvec(bits, W, s, b, x))
+    fm.batch_matvec(T(x, dev), specs)
+    torch.cuda.synchronize()
+    for sp, r in zip(specs, refs):
+        assert norm_err(sp[3].cpu().numpy(), r) <= TOL_F32
+
+
+@pytest.mark.parametrize("Tn,E,K,kind", [(1, 512, 10, "normal"), (512, 512, 10, "zipf"), (64, 512, 1, "normal"),
+                                         (16, 64, 64, "normal"), (8, 10, 10, "normal"), (32, 128, 16, "dup"),
+                                         (4, 4096, 8, "normal"), (3, 512, 20, "normal")])
+def test_route_topk(orc, dev, Tn, E, K, kind):
+    import torch
+    say("route", Tn, E, K, kind)
+    rng = synth.rng_for(5, Tn, E, K)
+    if kind == "zipf":
+        lg = synth.zipf_logits(rng, Tn, E)
+    elif kind == "dup":
+        lg = np.round(rng.normal(0, 1, (Tn, E)), 1).astype(np.float32)
+    else:
+        lg = rng.normal(0, 1, (Tn, E)).astype(np.float32)
+    idx = torch.empty((Tn, K), dtype=torch.int32, device=dev)
+    w = torch.empty((Tn, K), dtype=torch.float32, device=dev)
+    fm.route_topk(T(lg, dev), K, idx, w)
+    torch.cuda.synchronize()
+    ri, rw = orc.route(lg, K)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    assert norm_err(w.cpu().numpy(), rw) <= 1e-5
+
+
+def _decode_inputs(seed, K, bits_list, hidden=HIDDEN, inter=INTER):
+    rng = synth.rng_for(6, seed)
+    blobs = experts(range(seed * 100, seed * 100 + K + 1), bits_list, hidden, inter)
+    x = synth.hidden_vec(rng, hidden)
+    hm = rng.normal(0, 1, hidden).astype(np.float32)
+    lg = rng.normal(0, 1, 512).astype(np.float32)
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    w = np.sort(p)[-K:][::-1].astype(np.float32)
+    w /= w.sum()
+    return blobs, x, hm, w, float(rng.normal())
+
+
+@pytest.mark.parametrize("K,bitmode,hidden,inter", [(10, "4", HIDDEN, INTER), (10, "tiered", HIDDEN, INTER),
+                                                     (1, "4", HIDDEN, INTER), (16, "2", HIDDEN, INTER),
+                                                     (4, "4", 2048, 512), (3, "tiered", 1024, 2048)])
+def test_moe_decode_host_routed(orc, dev, K, bitmode, hidden, inter):
+    import torch
+    say("moe_decode", K, bitmode, hidden, inter)
+    bl = [4 if bitmode == "4" else 2 if bitmode == "2" else (4 if i % 3 == 0 else 2) for i in range(K + 1)]
+    blobs, x, hm, w, score = _decode_inputs(K + hidden // 512, K, bl, hidden, inter)
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, bl[i], hidden, inter) for i, db in enumerate(dblobs)]
+    ws = torch.empty(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    out = torch.empty(hidden, dtype=torch.float32, device=dev)
+    ob = torch.empty(hidden, dtype=torch.int16, device=dev)
+    fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, hidden, inter, shared=ex[K], shared_bits=bl[K],
+                  shared_score=score, h_mid=T(hm, dev), out_bf16=ob)
+    torch.cuda.synchronize()
+    ref = orc.moe_decode(blobs[:K], bl[:K], w, x, hidden, inter, shared_blob=blobs[K], shared_bits=bl[K],
+                         shared_score=score, h_mid=hm)
+    # compare the MoE contribution (out - h_mid) so the residual does not mask errors
+    got = out.cpu().numpy()
+    assert norm_err(got - hm, ref - hm) <= TOL_F32
+    assert norm_err(bf16_out(ob.cpu().numpy()), ref) <= TOL_BF16
+
+
+def test_moe_decode_valid_mask_and_no_shared(orc, dev):
+    import torch
+    say("moe_decode valid mask")
+    K = 6
+    bl = [4] * (K + 1)
+    blobs, x, hm, w, _ = _decode_inputs(77, K, bl)
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, 4, HIDDEN, INTER) for db in dblobs]
+    valid = [1, 0, 1, 1, 0, 1]
+    ws = torch.empty(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, valid=valid)
+    torch.cuda.synchronize()
+    ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, valid=valid)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_encode_experts_batched_and_combine(orc, dev):
+    import torch
+    say("encode_experts_batched + combine")
+    K = 4
+    bl = [4, 2, 4, 4, 2]
+    blobs, x, hm, w, score = _decode_inputs(12, K, bl)
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
+    ws = torch.empty(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    eo = torch.zeros((K + 1, HIDDEN), dtype=torch.float32, device=dev)
+    fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
+    torch.cuda.synchronize()
+    eon = eo.cpu().numpy()
+    for k in range(K + 1):
+        r = orc.expert_forward(blobs[k], bl[k], HIDDEN, INTER, x)
+        assert norm_err(eon[k], r) <= TOL_F32, k
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    sc = torch.tensor([score], dtype=torch.float32, device=dev)
+    fm.moe_combine(eo, T(w, dev), out, K, h_mid=T(hm, dev), shared_out=eo[K], shared_score=sc)
+    torch.cuda.synchronize()
+    ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, shared_blob=blobs[K], shared_bits=bl[K],
+                         shared_score=score, h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+@pytest.fixture(scope="module")
+def pool64(dev):
+    """64 experts, tiered 4/2-bit (every fourth expert 4-bit), plus a shared expert."""
+    E = 64
+    bits = [4 if e % 4 == 0 else 2 for e in range(E)]
+    blobs = experts(range(3000, 3000 + E), bits)
+    return blobs, bits, fm.DevicePool(blobs, bits, HIDDEN, INTER)
+
+
+def test_moe_decode_pool_device_routing(orc, dev, pool64):
+    import torch
+    say("moe_decode_pool")
+    blobs, bits, pool = pool64
+    K = 10
+    rng = synth.rng_for(13)
+    lg = rng.normal(0, 1, (1, 64)).astype(np.float32)
+    x = synth.hidden_vec(rng, HIDDEN)
+    hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+    shared_blob = synth.expert_blob((4000, 1), HIDDEN, INTER, 4)
+    dsh = T(shared_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
+    g = np.float32(0.3)
+    idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+    w = torch.empty((1, K), dtype=torch.float32, device=dev)
+    fm.route_topk(T(lg, dev), K, idx, w)
+    ws = torch.empty(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_decode_pool(pool, idx, w, T(x, dev), out, ws, shared=sh, shared_bits=4,
+                       shared_score=T(np.array([g]), dev), h_mid=T(hm, dev))
+    torch.cuda.synchronize()
+    ri, rw = orc.route(lg, K)
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                         shared_blob=shared_blob, shared_bits=4, shared_score=float(g), h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+def test_moe_forward_layer(orc, dev, pool64):
+    """Host C layer driver: router matvec -> device routing -> fused experts."""
+    import torch
+    say("moe_forward")
+    blobs, bits, pool = pool64
+    K = 8
+    rng = synth.rng_for(14)
+    Wr, sr, br = matrix(900, 64, HIDDEN, 4)
+    Wg, sg, bg = matrix(901, 1, HIDDEN, 4)
+    shared_blob = synth.expert_blob((4000, 2), HIDDEN, INTER, 4)
+    dsh = T(shared_blob, dev)
+    hp = synth.hidden_vec(rng, HIDDEN)
+    hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+    d = [T(a, dev) for a in (Wr, sr, br, Wg, sg, bg)]
+    L = fm.MoeLayer()
+    L.router_w, L.router_s, L.router_b = d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr()
+    L.router_bits = 4
+    L.seg_w, L.seg_s, L.seg_b = d[3].data_ptr(), d[4].data_ptr(), d[5].data_ptr()
+    L.seg_bits = 4
+    L.shared = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
+    L.shared_bits = 4
+    L.has_shared = 1
+    L.pool = pool.c
+    ws = torch.empty(fm.moe_forward_workspace_bytes(L, K), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_forward(L, K, T(hp, dev), T(hm, dev), out, ws)
+    torch.cuda.synchronize()
+    logits = orc.matvec(4, Wr, sr, br, hp)
+    score = orc.matvec(4, Wg, sg, bg, hp)[0]
+    ri, rw = orc.route(logits, K)
+    ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], hp, HIDDEN, INTER,
+                         shared_blob=shared_blob, shared_bits=4, shared_score=float(score), h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
