@@ -63,7 +63,7 @@ def bench_decode(args, dev):
     hm = torch.from_numpy(rng.normal(0, 1, H).astype(np.float32)).to(dev)
     idx = torch.empty((nsteps, K), dtype=torch.int32, device=dev)
     w = torch.empty((nsteps, K), dtype=torch.float32, device=dev)
-    ws = torch.empty(fm.decode_workspace_bytes(K + 1, H, I), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, H, I), dtype=torch.uint8, device=dev)
     out = torch.empty(H, dtype=torch.float32, device=dev)
     ob = torch.empty(H, dtype=torch.int16, device=dev)
 

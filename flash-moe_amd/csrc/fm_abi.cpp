@@ -80,3 +80,15 @@ extern "C" int fm_expert_from_blob(const void *blob, const fm_expert_layout *L,
     out->down_b = b + L->off[8];
     return FM_OK;
 }
+
+int fm_num_cus(void) {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}

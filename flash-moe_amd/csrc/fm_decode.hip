@@ -4,27 +4,29 @@
 // gpu_encode_experts_batched (gpu_dispatch.h:461-609: per expert a gate and an
 // up matvec, SwiGLU, a down matvec -- four dispatches per expert), the shared
 // expert's SwiGLU + down (layer_forward.h:3906-3937) and moe_combine_residual
-// (shaders.metal:1865-1900).  Here the whole step is two launches:
+// (shaders.metal:1865-1900).  Here the whole step is ONE kernel launch:
 //
-//  A  fm_decode_gateup_kernel: every (slot, row-block) of every expert's gate
-//     and up projection in one grid; SwiGLU in the epilogue; act[slot][inter]
-//     (fp32) to the workspace.  Gate and up rows of the same index are done by
-//     the same lanes so silu(g)*u needs no extra pass.
-//  B  fm_decode_down_kernel: one block per run of output rows; one wavefront
-//     per expert slot computes that slot's down-projection rows, the block
-//     then combines the slots in the reference order
-//       out = h_mid + sum_k w_k e_k + sigmoid(g) * shared
-//     (layer_forward.h:1257, 1295-1305) with no atomics, so results are
-//     deterministic and there is no K <= 8 limit.
+//  A  gate/up row passes of every slot (routed experts + shared), SwiGLU in
+//     the epilogue -> activations;
+//  B  down-projection row passes of every slot -> per-slot outputs y_k;
+//  C  combine, in the slot order of cpu_vec_madd (layer_forward.h:1257,
+//     1295-1305):  out = h_mid + sum_k w_k y_k + sigmoid(g) * y_shared.
+//
+// A persistent grid (sized to what stays resident) gives every wave an equal
+// share of the slot-major A and B passes.  Values handed from one wave to
+// another (activations, y_k) travel as 64-bit (value, epoch) words written
+// and read with agent-coherent accesses; consumers poll exactly the words
+// they need.  No atomics, no cache flushes, no K <= 8 limit, deterministic.
 //
 // Slots are described either on the host (kernel arguments) or, in pool mode,
 // resolved on the device from routing indices (no host round trip).
 #include "fm_device.h"
 #include "fm_internal.h"
 
+#include <atomic>
+
 #define FM_MAX_SLOTS (FM_MAX_K + 1)
-#define FM_A_NP 2  // rows per wave in phase A
-#define FM_B_NP 4  // row passes per wave in phase B
+#define FM_DECODE_BLOCKS_PER_CU 4  // persistent 256-thread blocks per CU (cap)
 
 struct FmSlot {
     const uint32_t *gw, *uw, *dw;
@@ -53,11 +55,14 @@ struct FmDecodeArgs {
     float shared_w_host;       // used when shared_score == NULL and host mode
     const float *shared_score; // device scalar (pre-sigmoid) or NULL
     const float *x;
-    float *act;
     const float *h_mid;
     float *out;
     uint16_t *out_bf16;
     float *expert_out;
+    uint64_t *act2;  // [S][inter]  (value bits | epoch << 32) SwiGLU activations
+    uint64_t *y2;    // [S][hidden] (value bits | epoch << 32) per-slot down outputs
+    uint32_t *err;   // set when a bounded wait gave up
+    uint32_t epoch;  // this call's tag (never 0)
 };
 
 __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
@@ -88,177 +93,616 @@ __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
     return s;
 }
 
+// Cross-wave hand-off without atomics read-modify-writes or cache
+// maintenance.  Every handed-off value is stored together with this call's
+// epoch as ONE 64-bit agent-coherent store (global_store_dwordx2 sc1); a
+// consumer polls the 64-bit words it needs with agent-coherent loads until
+// every tag equals the epoch.  No counters (which would serialise thousands of
+// device-scope atomics on one cache line), no L2 write-back/invalidate, and no
+// reset: a new call simply uses a new epoch.
+__device__ __forceinline__ void fm_put_tagged(uint64_t *p, float v, uint32_t epoch) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+#define FM_SPIN_MAX (1u << 16)
+
 // ---------------------------------------------------------------- phase A --
+// Persistent stream over the (slot, row-pass) units of every expert's gate and
+// up projections.  Each block stages x (fp32) and the slot descriptors in LDS
+// once; each wavefront owns a contiguous run of units, keeps its slice of x in
+// VGPRs as fp16 pairs, and issues the loads of unit u+1 before computing unit
+// u, so every wave always has a row-pair of packed weights in flight.
 template <int BITS, int LPR, int GPL>
-__device__ __forceinline__ void fm_gateup_body(const FmDecodeArgs &a, const FmSlot &s, int slot,
-                                               uint32_t row0) {
-    constexpr int RPP = 64 / LPR;
+struct FmGateUpBuf {
+    FmWGroup g[GPL], u[GPL];
+    float gs[GPL], gb[GPL], us[GPL], ub[GPL];
+};
+
+template <int BITS, int LPR, int GPL>
+__device__ __forceinline__ void fm_gateup_load(const FmSlot &s, uint32_t row, uint32_t hidden, uint32_t inter,
+                                               FmGateUpBuf<BITS, LPR, GPL> &b) {
     constexpr int WPG = 2 * BITS;
+    const int gl = (threadIdx.x & 63) % LPR;
+    const uint32_t G = hidden / 64;
+    const uint32_t wpr = hidden * BITS / 32;
+#pragma unroll
+    for (int j = 0; j < GPL; j++) {
+        uint32_t g = gl + j * LPR;
+        if (row < inter && g < G) {
+            size_t wo = (size_t)row * wpr + g * WPG, so = (size_t)row * G + g;
+            fm_load_wgroup<BITS>(s.gw + wo, b.g[j]);
+            fm_load_wgroup<BITS>(s.uw + wo, b.u[j]);
+            b.gs[j] = fm_bf16_to_f32(fm_ldg_u16(s.gs + so));
+            b.gb[j] = fm_bf16_to_f32(fm_ldg_u16(s.gb + so));
+            b.us[j] = fm_bf16_to_f32(fm_ldg_u16(s.us + so));
+            b.ub[j] = fm_bf16_to_f32(fm_ldg_u16(s.ub + so));
+        }
+    }
+}
+
+template <int BITS, int LPR, int GPL>
+__device__ __forceinline__ void fm_gateup_segment(const FmDecodeArgs &a, const FmSlot &s, int slot,
+                                                  const float *xs, uint32_t ubeg, uint32_t uend) {
+    constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, gl = lane % LPR;
     const uint32_t G = a.hidden / 64;
-    const uint32_t wpr = a.hidden * BITS / 32;
-
     FmXGroup xg[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; j++) {
         uint32_t g = gl + j * LPR;
-        if (g < G) fm_load_xgroup<BITS>(a.x + 64 * g, xg[j]);
+        if (g < G) fm_load_xgroup<BITS>(xs + 64 * g, xg[j]);
     }
-    FmWGroup wg[FM_A_NP][GPL], wu[FM_A_NP][GPL];
-    float gs[FM_A_NP][GPL], gb[FM_A_NP][GPL], us[FM_A_NP][GPL], ub[FM_A_NP][GPL];
-#pragma unroll
-    for (int p = 0; p < FM_A_NP; p++) {
-        uint32_t row = row0 + p * RPP + sub;
-#pragma unroll
-        for (int j = 0; j < GPL; j++) {
-            uint32_t g = gl + j * LPR;
-            if (row < a.inter && g < G) {
-                size_t wo = (size_t)row * wpr + g * WPG, so = (size_t)row * G + g;
-                fm_load_wgroup<BITS>(s.gw + wo, wg[p][j]);
-                fm_load_wgroup<BITS>(s.uw + wo, wu[p][j]);
-                gs[p][j] = fm_bf16_to_f32(s.gs[so]);
-                gb[p][j] = fm_bf16_to_f32(s.gb[so]);
-                us[p][j] = fm_bf16_to_f32(s.us[so]);
-                ub[p][j] = fm_bf16_to_f32(s.ub[so]);
-            }
-        }
-    }
-#pragma unroll
-    for (int p = 0; p < FM_A_NP; p++) {
-        uint32_t row = row0 + p * RPP + sub;
+    FmGateUpBuf<BITS, LPR, GPL> cur, nxt;
+    fm_gateup_load<BITS, LPR, GPL>(s, ubeg * RPP + sub, a.hidden, a.inter, cur);
+    for (uint32_t u = ubeg; u < uend; u++) {
+        const uint32_t row = u * RPP + sub;
+        if (u + 1 < uend) fm_gateup_load<BITS, LPR, GPL>(s, row + RPP, a.hidden, a.inter, nxt);
         float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int j = 0; j < GPL; j++) {
             uint32_t g = gl + j * LPR;
             if (row < a.inter && g < G) {
-                pg += fm_group_dot<BITS>(wg[p][j], xg[j], gs[p][j], gb[p][j]);
-                pu += fm_group_dot<BITS>(wu[p][j], xg[j], us[p][j], ub[p][j]);
+                pg += fm_group_dot<BITS>(cur.g[j], xg[j], cur.gs[j], cur.gb[j]);
+                pu += fm_group_dot<BITS>(cur.u[j], xg[j], cur.us[j], cur.ub[j]);
             }
         }
         pg = fm_lane_sum<LPR>(pg);
         pu = fm_lane_sum<LPR>(pu);
-        if (gl == 0 && row < a.inter) a.act[(size_t)slot * a.inter + row] = fm_silu_mul(pg, pu);
+        if (gl == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)slot * a.inter + row], fm_silu_mul(pg, pu), a.epoch);
+        cur = nxt;
     }
-}
-
-template <int LPR, int GPL>
-__global__ __launch_bounds__(256) void fm_decode_gateup_kernel(FmDecodeArgs a, uint32_t blocks_per_slot) {
-    constexpr int RPP = 64 / LPR;
-    constexpr int RB = 4 * FM_A_NP * RPP;
-    const int slot = blockIdx.x / blocks_per_slot;
-    const uint32_t rb = blockIdx.x % blocks_per_slot;
-    if (slot >= a.S) return;
-    const FmSlot s = fm_get_slot(a, slot);
-    if (!s.valid) return;
-    const uint32_t row0 = rb * RB + (threadIdx.x >> 6) * (FM_A_NP * RPP);
-    if (s.bits == 4)
-        fm_gateup_body<4, LPR, GPL>(a, s, slot, row0);
-    else
-        fm_gateup_body<2, LPR, GPL>(a, s, slot, row0);
 }
 
 // ---------------------------------------------------------------- phase B --
-// Returns this lane's row partial sums for FM_B_NP passes of one slot (valid in
-// lanes with gl == 0 after the reduction).
+// Down projection, streamed like phase A: (slot, 4-row pass) units, slot-major.
+// The lane's group of the slot's SwiGLU activation is read once per segment
+// (fp32 from the workspace, converted to the slot's fp16 pair layout).
 template <int BITS, int LPR, int GPL>
-__device__ __forceinline__ void fm_down_body(const FmDecodeArgs &a, const FmSlot &s, int slot,
-                                             uint32_t row0, float (&res)[FM_B_NP]) {
-    constexpr int RPP = 64 / LPR;
-    constexpr int WPG = 2 * BITS;
-    const int lane = threadIdx.x & 63;
-    const int sub = lane / LPR, gl = lane % LPR;
-    const uint32_t G = a.inter / 64;
-    const uint32_t wpr = a.inter * BITS / 32;
+struct FmDownBuf {
+    FmWGroup w[GPL];
+    float s[GPL], b[GPL];
+};
 
-    FmWGroup wd[FM_B_NP][GPL];
-    float ds[FM_B_NP][GPL], db[FM_B_NP][GPL];
-#pragma unroll
-    for (int p = 0; p < FM_B_NP; p++) {
-        uint32_t row = row0 + p * RPP + sub;
-#pragma unroll
-        for (int j = 0; j < GPL; j++) {
-            uint32_t g = gl + j * LPR;
-            if (row < a.hidden && g < G) {
-                fm_load_wgroup<BITS>(s.dw + (size_t)row * wpr + g * WPG, wd[p][j]);
-                ds[p][j] = fm_bf16_to_f32(s.ds[(size_t)row * G + g]);
-                db[p][j] = fm_bf16_to_f32(s.db[(size_t)row * G + g]);
-            }
-        }
-    }
-    FmXGroup xg[GPL];
-    const float *act = a.act + (size_t)slot * a.inter;
+template <int BITS, int LPR, int GPL>
+__device__ __forceinline__ void fm_down_load(const FmSlot &s, uint32_t row, uint32_t hidden, uint32_t inter,
+                                             FmDownBuf<BITS, LPR, GPL> &b) {
+    constexpr int WPG = 2 * BITS;
+    const int gl = (threadIdx.x & 63) % LPR;
+    const uint32_t G = inter / 64;
+    const uint32_t wpr = inter * BITS / 32;
 #pragma unroll
     for (int j = 0; j < GPL; j++) {
         uint32_t g = gl + j * LPR;
-        if (g < G) fm_load_xgroup<BITS>(act + 64 * g, xg[j]);
+        if (row < hidden && g < G) {
+            size_t so = (size_t)row * G + g;
+            fm_load_wgroup<BITS>(s.dw + (size_t)row * wpr + g * WPG, b.w[j]);
+            b.s[j] = fm_bf16_to_f32(fm_ldg_u16(s.ds + so));
+            b.b[j] = fm_bf16_to_f32(fm_ldg_u16(s.db + so));
+        }
     }
+}
+
+// y[row] for rows of passes [pbeg, pend) of one slot; writes `dst` (fp32,
+// indexed by row) from the first lane of each row segment.
+template <int BITS, int LPR, int GPL>
+__device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmSlot &s, int slot,
+                                                uint32_t pbeg, uint32_t pend, float *dst, float *wbuf) {
+    constexpr int RPP = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / LPR, gl = lane % LPR;
+    const uint32_t G = a.inter / 64;
+    FmDownBuf<BITS, LPR, GPL> cur, nxt;
+    fm_down_load<BITS, LPR, GPL>(s, pbeg * RPP + sub, a.hidden, a.inter, cur);
+    // The slot's activation: poll its tagged words (coalesced, agent-coherent)
+    // until all carry this call's epoch, then stage the values in this wave's
+    // LDS buffer so each lane can pick up its own groups.
+    const uint64_t *act = a.act2 + (size_t)slot * a.inter;
+    for (uint32_t i0 = 0; i0 < a.inter; i0 += 64) {
+        const uint32_t i = i0 + lane;
+        uint64_t v = i < a.inter ? fm_get_tagged(act + i) : ((uint64_t)a.epoch << 32);
+        uint32_t it = 0;
+        while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+            __builtin_amdgcn_s_sleep(1);
+            if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(act + i);
+        }
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (i < a.inter) wbuf[i] = __uint_as_float((uint32_t)v);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    FmXGroup xg[GPL];
 #pragma unroll
-    for (int p = 0; p < FM_B_NP; p++) {
-        uint32_t row = row0 + p * RPP + sub;
+    for (int j = 0; j < GPL; j++) {
+        uint32_t g = gl + j * LPR;
+        if (g < G) fm_load_xgroup<BITS>(wbuf + 64 * g, xg[j]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t p = pbeg; p < pend; p++) {
+        const uint32_t row = p * RPP + sub;
+        if (p + 1 < pend) fm_down_load<BITS, LPR, GPL>(s, row + RPP, a.hidden, a.inter, nxt);
         float part = 0.f;
 #pragma unroll
         for (int j = 0; j < GPL; j++) {
             uint32_t g = gl + j * LPR;
-            if (row < a.hidden && g < G) part += fm_group_dot<BITS>(wd[p][j], xg[j], ds[p][j], db[p][j]);
+            if (row < a.hidden && g < G) part += fm_group_dot<BITS>(cur.w[j], xg[j], cur.s[j], cur.b[j]);
         }
-        res[p] = fm_lane_sum<LPR>(part);
+        part = fm_lane_sum<LPR>(part);
+        if (gl == 0 && row < a.hidden) {
+            if (a.mode == 1)
+                dst[row] = part;
+            else
+                fm_put_tagged(&a.y2[(size_t)slot * a.hidden + row], part, a.epoch);
+        }
+        cur = nxt;
     }
 }
 
-template <int LPR, int GPL>
-__global__ __launch_bounds__(1024) void fm_decode_down_kernel(FmDecodeArgs a) {
-    constexpr int RPP = 64 / LPR;
-    constexpr int RB = FM_B_NP * RPP;  // rows per block (every wave covers all of them)
-    __shared__ float part[FM_MAX_SLOTS][RB];
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+// ----------------------------------------------------------- fused kernel --
+// One launch for the whole expert step.  The grid is sized to what the GPU
+// keeps resident at once, so every wave a consumer waits on is running; each
+// wait is bounded anyway (FM_SPIN_MAX polls) and a give-up raises *err.
+//
+// Wave w owns the same fraction of the slot-major A units (gate/up row passes)
+// and B units (down row passes), so its B work belongs to the slot whose
+// activations it just helped produce.  The wave that computes the LAST slot's
+// down rows for a pass also combines those rows:
+//   out = h_mid + sum_{k<K} w_k y_k + sigmoid(g) y_shared
+// in the slot order of cpu_vec_madd (layer_forward.h:1257, 1295-1305), polling
+// the other slots' tagged y words for the pass's rows first.
+template <int RPP>
+__device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, const FmSlot *sd, uint32_t row0, float sw,
+                                                float *stage) {
     const int lane = threadIdx.x & 63;
-    const int sub = lane / LPR, gl = lane % LPR;
-    const uint32_t row0 = blockIdx.x * RB;
-
-    for (int k = wave; k < a.S; k += nw) {
-        const FmSlot s = fm_get_slot(a, k);
-        float res[FM_B_NP];
-        if (s.valid) {
-            if (s.bits == 4)
-                fm_down_body<4, LPR, GPL>(a, s, k, row0, res);
-            else
-                fm_down_body<2, LPR, GPL>(a, s, k, row0, res);
-        } else {
-#pragma unroll
-            for (int p = 0; p < FM_B_NP; p++) res[p] = 0.f;
+    const int n = (a.S - 1) * RPP;  // values to collect from other slots
+    for (int base = 0; base < n; base += 64) {
+        const int q = base + lane;
+        const int k = q / RPP, r = q % RPP;
+        const bool need = q < n && sd[k].valid && row0 + r < a.hidden;
+        uint64_t v = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]) : ((uint64_t)a.epoch << 32);
+        uint32_t it = 0;
+        while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+            __builtin_amdgcn_s_sleep(1);
+            if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]);
         }
-        if (gl == 0) {
-#pragma unroll
-            for (int p = 0; p < FM_B_NP; p++) {
-                uint32_t r = p * RPP + sub;
-                if (a.mode == 1) {
-                    uint32_t row = row0 + r;
-                    if (s.valid && row < a.hidden) a.expert_out[(size_t)k * a.hidden + row] = res[p];
-                } else {
-                    part[k][r] = res[p];
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (q < n) stage[q] = need ? __uint_as_float((uint32_t)v) : 0.f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    if (lane < RPP && row0 + lane < a.hidden) {
+        const uint32_t row = row0 + lane;
+        const float ylast = stage[(a.S - 1) * RPP + lane];
+        float moe = 0.f;
+        for (int k = 0; k < a.K; k++) {
+            const float yk = k == a.S - 1 ? ylast : stage[k * RPP + lane];
+            if (sd[k].valid) moe = __fadd_rn(moe, __fmul_rn(sd[k].weight, yk));
+        }
+        float v = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+        if (a.has_shared) v = __fadd_rn(v, __fmul_rn(sw, ylast));
+        a.out[row] = v;
+        if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(v);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int LH, int GH, int LI, int GI>
+__global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, uint32_t nwaves) {
+    constexpr int RPPA = 64 / LH, RPPB = 64 / LI;
+    // LDS: x (hidden floats), then one inter-float buffer per wave
+    extern __shared__ float xs[];
+    __shared__ FmSlot sd[FM_MAX_SLOTS];
+    if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
+    for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    float *wbuf = xs + a.hidden + (threadIdx.x >> 6) * a.inter;
+
+    // ---- A: gate/up + SwiGLU -> tagged act ----
+    const uint32_t upsA = (a.inter + RPPA - 1) / RPPA;
+    const uint64_t NA = (uint64_t)a.S * upsA;
+    uint32_t u = (uint32_t)(NA * w / nwaves);
+    const uint32_t u1 = (uint32_t)(NA * (w + 1) / nwaves);
+    while (u < u1) {
+        const int k = u / upsA;
+        const uint32_t seg_end = min(u1, (uint32_t)(k + 1) * upsA);
+        const FmSlot s = sd[k];
+        if (s.valid) {
+            const uint32_t b = u - k * upsA, e = seg_end - k * upsA;
+            if (s.bits == 4)
+                fm_gateup_segment<4, LH, GH>(a, s, k, xs, b, e);
+            else
+                fm_gateup_segment<2, LH, GH>(a, s, k, xs, b, e);
+        }
+        u = seg_end;
+    }
+
+    // ---- B: down projection -> tagged y; the last slot's waves combine ----
+    const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+    const uint32_t upsB = (a.hidden + RPPB - 1) / RPPB;
+    const uint64_t NB = (uint64_t)a.S * upsB;
+    uint32_t v = (uint32_t)(NB * w / nwaves);
+    const uint32_t v1 = (uint32_t)(NB * (w + 1) / nwaves);
+    while (v < v1) {
+        const int k = v / upsB;
+        const uint32_t seg_end = min(v1, (uint32_t)(k + 1) * upsB);
+        const uint32_t pb = v - k * upsB, pe = seg_end - k * upsB;
+        const FmSlot s = sd[k];
+        if (s.valid) {
+            float *dst = a.mode == 1 ? a.expert_out + (size_t)k * a.hidden : nullptr;
+            if (s.bits == 4)
+                fm_down_segment<4, LI, GI>(a, s, k, pb, pe, dst, wbuf);
+            else
+                fm_down_segment<2, LI, GI>(a, s, k, pb, pe, dst, wbuf);
+        }
+        if (a.mode == 0 && k == a.S - 1) {
+            for (uint32_t p = pb; p < pe; p++) {
+                // the last slot's own y for this pass (if valid) is read back tagged too
+                if (s.valid) {
+                    const uint32_t row = p * RPPB + (lane < RPPB ? lane : 0);
+                    uint64_t t = lane < RPPB && row < a.hidden ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row])
+                                                               : ((uint64_t)a.epoch << 32);
+                    uint32_t it = 0;
+                    while (!__all((uint32_t)(t >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+                        __builtin_amdgcn_s_sleep(1);
+                        if ((uint32_t)(t >> 32) != a.epoch) t = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]);
+                    }
+                    if (lane < RPPB) wbuf[(a.S - 1) * RPPB + lane] = __uint_as_float((uint32_t)t);
+                } else if (lane < RPPB) {
+                    wbuf[(a.S - 1) * RPPB + lane] = 0.f;
                 }
+                fm_combine_pass<RPPB>(a, sd, p * RPPB, sw, wbuf);
+            }
+        }
+        v = seg_end;
+    }
+}
+
+// ------------------------------------------------- fused kernel, eager loads --
+// Fast path for rows of one group per lane (hidden, inter <= 4096).  Each wave
+// owns <= UMAX gate/up units and <= UMAX down units and issues ALL of their
+// weight loads before any compute -- weights never depend on activations, so
+// the whole 78 MB stream is in flight from the first microsecond and the
+// memory system, not a chain of per-wave round trips, sets the pace.  Compute
+// then follows the data in issue order.  Between the phases the block stages
+// the activations of its (at most two) down-projection slots once in LDS.
+#define FM_UMAX 6
+
+struct FmUnitW {
+    FmWGroup w;
+    float s, b;
+};
+
+__device__ __forceinline__ void fm_unit_load(const uint32_t *W, const uint16_t *S, const uint16_t *B, int bits,
+                                             uint32_t row, uint32_t in_dim, uint32_t g, bool ok, FmUnitW &u) {
+    if (!ok) return;
+    const uint32_t G = in_dim / 64;
+    const uint32_t wpr = in_dim * bits / 32;
+    const uint32_t *wp = W + (size_t)row * wpr + g * 2 * bits;
+    u.w.a = fm_ldg_u4_nt(wp);
+    if (bits == 4) u.w.b = fm_ldg_u4_nt(wp + 4);
+    u.s = fm_bf16_to_f32(fm_ldg_u16(S + (size_t)row * G + g));
+    u.b = fm_bf16_to_f32(fm_ldg_u16(B + (size_t)row * G + g));
+}
+
+__device__ __forceinline__ float fm_unit_dot(const FmUnitW &u, const FmXGroup &x, int bits) {
+    return bits == 4 ? fm_group_dot<4>(u.w, x, u.s, u.b) : fm_group_dot<2>(u.w, x, u.s, u.b);
+}
+
+__device__ __forceinline__ void fm_xgroup_bits(const float *src, int bits, FmXGroup &x) {
+    if (bits == 4)
+        fm_load_xgroup<4>(src, x);
+    else
+        fm_load_xgroup<2>(src, x);
+}
+
+// gate and up group dots with four independent accumulator chains
+template <int BITS>
+__device__ __forceinline__ void fm_dot_gu(const FmUnitW &g, const FmUnitW &u, const FmXGroup &x, float &pg,
+                                          float &pu) {
+    float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+    if constexpr (BITS == 4) {
+        const uint32_t gw[8] = {g.w.a.x, g.w.a.y, g.w.a.z, g.w.a.w, g.w.b.x, g.w.b.y, g.w.b.z, g.w.b.w};
+        const uint32_t uw[8] = {u.w.a.x, u.w.a.y, u.w.a.z, u.w.a.w, u.w.b.x, u.w.b.y, u.w.b.z, u.w.b.w};
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const uint32_t a = gw[p], b = uw[p], ta = a >> 8, tb = b >> 8;
+            const fm_h2 *q = &x.q[4 * p];
+            g0 = fm_dot2(fm_as_h2(a & 0x000F000Fu), q[0], g0);
+            u0 = fm_dot2(fm_as_h2(b & 0x000F000Fu), q[0], u0);
+            g1 = fm_dot2(fm_as_h2(a & 0x00F000F0u), q[1], g1);
+            u1 = fm_dot2(fm_as_h2(b & 0x00F000F0u), q[1], u1);
+            g0 = fm_dot2(fm_as_h2(ta & 0x000F000Fu), q[2], g0);
+            u0 = fm_dot2(fm_as_h2(tb & 0x000F000Fu), q[2], u0);
+            g1 = fm_dot2(fm_as_h2(ta & 0x00F000F0u), q[3], g1);
+            u1 = fm_dot2(fm_as_h2(tb & 0x00F000F0u), q[3], u1);
+        }
+    } else {
+        const uint32_t gw[4] = {g.w.a.x, g.w.a.y, g.w.a.z, g.w.a.w};
+        const uint32_t uw[4] = {u.w.a.x, u.w.a.y, u.w.a.z, u.w.a.w};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const fm_h2 *q = &x.q[8 * p];
+            g0 = fm_dot_word2(gw[p], q, g0);
+            u0 = fm_dot_word2(uw[p], q, u0);
+        }
+    }
+    pg = __builtin_fmaf(g.s * 16777216.0f, g0 + g1, g.b * x.sum);
+    pu = __builtin_fmaf(u.s * 16777216.0f, u0 + u1, u.b * x.sum);
+}
+
+// one group dot with four accumulator chains
+template <int BITS>
+__device__ __forceinline__ float fm_dot_one(const FmUnitW &g, const FmXGroup &x) {
+    float c0 = 0.f, c1 = 0.f, c2 = 0.f, c3 = 0.f;
+    if constexpr (BITS == 4) {
+        const uint32_t gw[8] = {g.w.a.x, g.w.a.y, g.w.a.z, g.w.a.w, g.w.b.x, g.w.b.y, g.w.b.z, g.w.b.w};
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const uint32_t a = gw[p], ta = a >> 8;
+            const fm_h2 *q = &x.q[4 * p];
+            c0 = fm_dot2(fm_as_h2(a & 0x000F000Fu), q[0], c0);
+            c1 = fm_dot2(fm_as_h2(a & 0x00F000F0u), q[1], c1);
+            c2 = fm_dot2(fm_as_h2(ta & 0x000F000Fu), q[2], c2);
+            c3 = fm_dot2(fm_as_h2(ta & 0x00F000F0u), q[3], c3);
+        }
+    } else {
+        const uint32_t gw[4] = {g.w.a.x, g.w.a.y, g.w.a.z, g.w.a.w};
+        c0 = fm_dot_word2(gw[0], &x.q[0], c0);
+        c1 = fm_dot_word2(gw[1], &x.q[8], c1);
+        c2 = fm_dot_word2(gw[2], &x.q[16], c2);
+        c3 = fm_dot_word2(gw[3], &x.q[24], c3);
+    }
+    return __builtin_fmaf(g.s * 16777216.0f, (c0 + c1) + (c2 + c3), g.b * x.sum);
+}
+
+template <int LH, int LI>
+__global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a, uint32_t nwaves) {
+    constexpr int RPPA = 64 / LH, RPPB = 64 / LI;
+    extern __shared__ float xs[];  // x [hidden] | act [2][inter] | combine stage [4][S*RPPB]
+    __shared__ FmSlot sd[FM_MAX_SLOTS];
+    float *acts = xs + a.hidden;
+    float *stage_all = acts + 2 * a.inter;
+    if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
+    for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t w = blockIdx.x * 4 + wv;
+    const int subA = lane / LH, glA = lane % LH;
+    const int subB = lane / LI, glB = lane % LI;
+
+    const uint32_t upsA = (a.inter + RPPA - 1) / RPPA;
+    const uint64_t NA = (uint64_t)a.S * upsA;
+    const uint32_t u0 = (uint32_t)(NA * w / nwaves), u1 = (uint32_t)(NA * (w + 1) / nwaves);
+    const uint32_t upsB = (a.hidden + RPPB - 1) / RPPB;
+    const uint64_t NB = (uint64_t)a.S * upsB;
+    const uint32_t v0 = (uint32_t)(NB * w / nwaves), v1 = (uint32_t)(NB * (w + 1) / nwaves);
+
+    // ---- issue every weight load of this wave ----
+    FmUnitW ga[FM_UMAX], ua[FM_UMAX];
+#pragma unroll
+    for (int i = 0; i < FM_UMAX; i++) {
+        const uint32_t u = u0 + i;
+        if (u < u1) {
+            const int k = u / upsA;
+            const FmSlot &s = sd[k];
+            const uint32_t row = (u - k * upsA) * RPPA + subA;
+            const bool ok = s.valid && row < a.inter && (uint32_t)glA < a.hidden / 64;
+            fm_unit_load(s.gw, s.gs, s.gb, s.bits, row, a.hidden, glA, ok, ga[i]);
+            fm_unit_load(s.uw, s.us, s.ub, s.bits, row, a.hidden, glA, ok, ua[i]);
+        }
+    }
+    // ---- A: gate/up + SwiGLU -> tagged act ----
+    FmXGroup xg;
+    int xbits = 0;
+#pragma unroll
+    for (int i = 0; i < FM_UMAX; i++) {
+        const uint32_t u = u0 + i;
+        if (u < u1) {
+            const int k = u / upsA;
+            const FmSlot &s = sd[k];
+            if (s.valid) {
+                if (s.bits != xbits) {
+                    xbits = s.bits;
+                    if ((uint32_t)glA < a.hidden / 64) fm_xgroup_bits(xs + 64 * glA, xbits, xg);
+                }
+                const uint32_t row = (u - k * upsA) * RPPA + subA;
+                const bool ok = row < a.inter && (uint32_t)glA < a.hidden / 64;
+                float pg = 0.f, pu = 0.f;
+                if (ok) {
+                    if (s.bits == 4) {
+                        fm_dot_gu<4>(ga[i], ua[i], xg, pg, pu);
+                    } else {
+                        fm_dot_gu<2>(ga[i], ua[i], xg, pg, pu);
+                    }
+                }
+                pg = fm_lane_sum<LH>(pg);
+                pu = fm_lane_sum<LH>(pu);
+                if (glA == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)k * a.inter + row], fm_silu_mul(pg, pu), a.epoch);
             }
         }
     }
-    if (a.mode == 1) return;
+
+    // ---- issue the down-projection weight loads (independent of act) ----
+    FmUnitW db[FM_UMAX];
+#pragma unroll
+    for (int i = 0; i < FM_UMAX; i++) {
+        const uint32_t v = v0 + i;
+        if (v < v1) {
+            const int k = v / upsB;
+            const FmSlot &s = sd[k];
+            const uint32_t row = (v - k * upsB) * RPPB + subB;
+            const bool ok = s.valid && row < a.hidden && (uint32_t)glB < a.inter / 64;
+            fm_unit_load(s.dw, s.ds, s.db, s.bits, row, a.inter, glB, ok, db[i]);
+        }
+    }
+
+    // ---- stage the block's down-projection slots' activations ----
+    const uint32_t bv0 = (uint32_t)(NB * (blockIdx.x * 4) / nwaves);
+    const uint32_t bv1 = (uint32_t)(NB * (blockIdx.x * 4 + 4) / nwaves);
+    const int kb0 = bv0 / upsB;
+    const int kb1 = bv1 > bv0 ? (bv1 - 1) / upsB : kb0;
+    {
+        // every thread issues all of its coherent loads for both slots at once,
+        // then re-polls only what was not yet tagged with this call's epoch
+        constexpr int MAXQ = 16;  // (2 slots x inter) / 256 threads, inter <= 2048
+        uint64_t t[MAXQ];
+        const int nslot = (kb1 < a.S ? kb1 : a.S - 1) - kb0 + 1;
+        const uint32_t total = (uint32_t)nslot * a.inter;
+#pragma unroll
+        for (int q = 0; q < MAXQ; q++) {
+            const uint32_t i = q * 256 + threadIdx.x;
+            const int kk = kb0 + (int)(i / a.inter);
+            const bool need = i < total && sd[kk].valid;
+            t[q] = need ? fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i) : ((uint64_t)a.epoch << 32);
+        }
+        uint32_t it = 0;
+        bool ready;
+        do {
+            ready = true;
+#pragma unroll
+            for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == a.epoch;
+            if (__all(ready)) break;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int q = 0; q < MAXQ; q++) {
+                const uint32_t i = q * 256 + threadIdx.x;
+                if ((uint32_t)(t[q] >> 32) != a.epoch) t[q] = fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i);
+            }
+        } while (++it < FM_SPIN_MAX);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+#pragma unroll
+        for (int q = 0; q < MAXQ; q++) {
+            const uint32_t i = q * 256 + threadIdx.x;
+            if (i < total) acts[i] = __uint_as_float((uint32_t)t[q]);
+        }
+    }
     __syncthreads();
-    if ((int)threadIdx.x < RB) {
-        const uint32_t r = threadIdx.x, row = row0 + r;
-        if (row < a.hidden) {
-            // cpu_vec_madd order: moe += w_k * e_k over k (layer_forward.h:1257)
-            float moe = 0.f;
-            for (int k = 0; k < a.K; k++) {
-                const FmSlot s = fm_get_slot(a, k);
-                if (s.valid) moe = __fadd_rn(moe, __fmul_rn(s.weight, part[k][r]));
+
+    // ---- B: down projection -> tagged y (or per-slot outputs) ----
+    const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+    float *stage = stage_all + wv * (FM_UMAX * a.S * RPPB);
+    xbits = 0;
+    int xslot = -1;
+#pragma unroll
+    for (int i = 0; i < FM_UMAX; i++) {
+        const uint32_t v = v0 + i;
+        if (v < v1) {
+            const int k = v / upsB;
+            const FmSlot &s = sd[k];
+            const uint32_t p = v - k * upsB;
+            const uint32_t row = p * RPPB + subB;
+            float y = 0.f;
+            if (s.valid) {
+                if (k != xslot || s.bits != xbits) {
+                    xslot = k;
+                    xbits = s.bits;
+                    if ((uint32_t)glB < a.inter / 64) fm_xgroup_bits(acts + (k - kb0) * a.inter + 64 * glB, xbits, xg);
+                }
+                const bool ok = row < a.hidden && (uint32_t)glB < a.inter / 64;
+                y = fm_lane_sum<LI>(ok ? (s.bits == 4 ? fm_dot_one<4>(db[i], xg) : fm_dot_one<2>(db[i], xg)) : 0.f);
+                if (glB == 0 && row < a.hidden) {
+                    if (a.mode == 1)
+                        a.expert_out[(size_t)k * a.hidden + row] = y;
+                    else if (k != a.S - 1)
+                        fm_put_tagged(&a.y2[(size_t)k * a.hidden + row], y, a.epoch);
+                }
             }
-            float v = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
-            if (a.has_shared) {
-                float sw = a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host;
-                v = __fadd_rn(v, __fmul_rn(sw, part[a.K][r]));
+            if (a.mode == 0 && k == a.S - 1 && glB == 0) stage[i * a.S * RPPB + (a.S - 1) * RPPB + subB] = y;
+        }
+    }
+
+    // ---- combine the passes whose last slot this wave computed ----
+    if (a.mode == 0) {
+        // units [v0, v1) of the last slot -> passes; gather other slots' y for
+        // all of them with one batch of coherent loads, re-poll stragglers
+        const int kl = a.S - 1;
+        const uint32_t lb = max(v0, (uint32_t)kl * upsB), le = min(v1, (uint32_t)(kl + 1) * upsB);
+        if (lb < le) {
+            const int nu = le - lb;
+            const int per = kl * RPPB;          // values per pass from other slots
+            const int n = nu * per;             // <= FM_UMAX * 16 * 4
+            constexpr int MAXQ = (FM_UMAX * FM_MAX_SLOTS * 4 + 63) / 64;
+            uint64_t t[MAXQ];
+#pragma unroll
+            for (int q = 0; q < MAXQ; q++) {
+                const int e = q * 64 + lane;
+                const int ui = e / (per > 0 ? per : 1), rem = e % (per > 0 ? per : 1);
+                const int k = rem / RPPB, r = rem % RPPB;
+                const uint32_t row = (lb + ui - kl * upsB) * RPPB + r;
+                const bool need = e < n && sd[k].valid && row < a.hidden;
+                t[q] = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]) : ((uint64_t)a.epoch << 32);
             }
-            a.out[row] = v;
-            if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(v);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == a.epoch;
+                if (__all(ready)) break;
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int q = 0; q < MAXQ; q++) {
+                    if ((uint32_t)(t[q] >> 32) != a.epoch) {
+                        const int e = q * 64 + lane;
+                        const int ui = e / per, rem = e % per;
+                        const int k = rem / RPPB, r = rem % RPPB;
+                        const uint32_t row = (lb + ui - kl * upsB) * RPPB + r;
+                        t[q] = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]);
+                    }
+                }
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+            // stage[ui][k][r] holds every slot's y for unit ui (slot kl written above)
+            const int i_of_lb = lb - v0;
+#pragma unroll
+            for (int q = 0; q < MAXQ; q++) {
+                const int e = q * 64 + lane;
+                if (e < n) {
+                    const int ui = e / per, rem = e % per;
+                    const int k = rem / RPPB, r = rem % RPPB;
+                    stage[(i_of_lb + ui) * a.S * RPPB + k * RPPB + r] =
+                        sd[k].valid ? __uint_as_float((uint32_t)t[q]) : 0.f;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            if (lane < nu * RPPB) {
+                const int ui = lane / RPPB, r = lane % RPPB;
+                const uint32_t row = (lb + ui - kl * upsB) * RPPB + r;
+                const float *st = stage + (i_of_lb + ui) * a.S * RPPB;
+                if (row < a.hidden) {
+                    float moe = 0.f;
+                    for (int k = 0; k < a.K; k++)
+                        if (sd[k].valid) moe = __fadd_rn(moe, __fmul_rn(sd[k].weight, st[k * RPPB + r]));
+                    float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+                    if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, st[kl * RPPB + r]));
+                    a.out[row] = o;
+                    if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+                }
+            }
         }
     }
 }
@@ -307,50 +751,101 @@ static int fm_check_expert(const char *who, int k, const fm_expert_weights &e, i
     return FM_OK;
 }
 
+// Workspace: [err word, 256 B] [act2: S x inter x 8 B] [y2: S x hidden x 8 B]
+// Tags make stale contents harmless, so the workspace needs no initialisation.
 extern "C" size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter) {
-    (void)hidden;
     if (n_slots < 1) n_slots = 1;
-    return fm_align_up((size_t)n_slots * inter * sizeof(float), 256);
+    return 256 + fm_align_up((size_t)n_slots * inter * 8, 256) + fm_align_up((size_t)n_slots * hidden * 8, 256);
+}
+
+static uint32_t fm_next_epoch() {
+    static std::atomic<uint32_t> ctr{0};
+    uint32_t e = ctr.fetch_add(1) + 1;
+    if (e == 0) e = ctr.fetch_add(1) + 1;  // 0 never tags anything
+    return e;
+}
+
+template <int LH, int GH, int LI, int GI>
+static int fm_launch_fused(FmDecodeArgs &a, hipStream_t st) {
+    auto kern = fm_decode_fused_kernel<LH, GH, LI, GI>;
+    const size_t lds = ((size_t)a.hidden + 4 * (size_t)a.inter) * sizeof(float);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1)
+        return fm_fail(FM_ERR_HIP, "fm_moe_decode: occupancy query failed");
+    if (per_cu > FM_DECODE_BLOCKS_PER_CU) per_cu = FM_DECODE_BLOCKS_PER_CU;
+    uint32_t blocks = (uint32_t)(fm_num_cus() * per_cu);
+    uint32_t nwaves = blocks * 4;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a, nwaves);
+    return fm_check_launch("fm_decode_fused_kernel");
+}
+
+template <int LH, int LI>
+static int fm_launch_eager_t(FmDecodeArgs &a, hipStream_t st) {
+    auto kern = fm_decode_eager_kernel<LH, LI>;
+    const size_t lds = ((size_t)a.hidden + 2 * (size_t)a.inter + 4 * FM_UMAX * (size_t)a.S * (64 / LI)) * sizeof(float);
+    if (a.inter > 2048) return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: inter");
+    if (lds > 65536) return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: LDS");
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1)
+        return fm_fail(FM_ERR_HIP, "fm_moe_decode: occupancy query failed");
+    if (per_cu > FM_DECODE_BLOCKS_PER_CU) per_cu = FM_DECODE_BLOCKS_PER_CU;
+    const uint32_t blocks = (uint32_t)(fm_num_cus() * per_cu);
+    const uint32_t nwaves = blocks * 4;
+    const uint64_t NA = (uint64_t)a.S * ((a.inter + 64 / LH - 1) / (64 / LH));
+    const uint64_t NB = (uint64_t)a.S * ((a.hidden + 64 / LI - 1) / (64 / LI));
+    // units per wave must fit the register-resident buffers, and one block's
+    // down units may span at most two slots
+    if ((NA + nwaves - 1) / nwaves > FM_UMAX || (NB + nwaves - 1) / nwaves > FM_UMAX)
+        return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: too many units per wave");
+    const uint64_t upsB = (a.hidden + 64 / LI - 1) / (64 / LI);
+    if (4 * ((NB + nwaves - 1) / nwaves) > upsB) return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: slot span");
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, a, nwaves);
+    return fm_check_launch("fm_decode_eager_kernel");
+}
+
+static int fm_launch_eager(FmDecodeArgs &a, int lh, int li, hipStream_t st) {
+#define FM_E(A, B) \
+    if (lh == A && li == B) return fm_launch_eager_t<A, B>(a, st);
+    FM_E(64, 16) FM_E(64, 32) FM_E(64, 64) FM_E(32, 16) FM_E(32, 32) FM_E(32, 64) FM_E(16, 16) FM_E(16, 32) FM_E(16, 64)
+#undef FM_E
+    return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: lanes");
 }
 
 static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const char *who = "fm_moe_decode";
     FM_REQUIRE(a.hidden % 64 == 0 && a.inter % 64 == 0 && a.hidden && a.inter,
                "%s: hidden %u / inter %u must be positive multiples of 64", who, a.hidden, a.inter);
-    int lh, gh, li, gi;
-    if (!fm_pick_lanes(a.hidden / 64, &lh, &gh) || !fm_pick_lanes(a.inter / 64, &li, &gi))
-        return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden %u / inter %u exceed 16384", who, a.hidden, a.inter);
     size_t need = fm_moe_decode_workspace_size(a.S, a.hidden, a.inter);
     if (!ws || ws_bytes < need)
         return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", who, ws_bytes, need);
     if ((uintptr_t)a.x & 15) return fm_fail(FM_ERR_INVALID, "%s: x not 16-byte aligned", who);
-    a.act = (float *)ws;
-
-    const uint32_t rba = 4u * FM_A_NP * (64u / lh);
-    const uint32_t bps = (a.inter + rba - 1) / rba;
-    dim3 ga((unsigned)(bps * a.S)), ba(256);
-#define FM_A_CASE(L, G)                                                                   \
-    if (lh == L && gh == G) {                                                             \
-        hipLaunchKernelGGL((fm_decode_gateup_kernel<L, G>), ga, ba, 0, st, a, bps);      \
-    } else
-    FM_A_CASE(16, 1) FM_A_CASE(32, 1) FM_A_CASE(64, 1) FM_A_CASE(64, 2) FM_A_CASE(64, 4) {
-        return fm_fail(FM_ERR_UNSUPPORTED, "%s: no gate/up kernel", who);
+    if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
+    FM_REQUIRE(a.S * 4 <= (int)a.inter, "%s: inter %u too small for %d slots", who, a.inter, a.S);
+    char *p = (char *)ws;
+    a.err = (uint32_t *)p;
+    p += 256;
+    a.act2 = (uint64_t *)p;
+    p += fm_align_up((size_t)a.S * a.inter * 8, 256);
+    a.y2 = (uint64_t *)p;
+    a.epoch = fm_next_epoch();
+    if (((size_t)a.hidden + 4 * (size_t)a.inter) * sizeof(float) > 65536)
+        return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden + 4*inter must be <= 16384 floats", who);
+    int lh, gh, li, gi;
+    if (!fm_pick_lanes(a.hidden / 64, &lh, &gh) || !fm_pick_lanes(a.inter / 64, &li, &gi) || gh > 2 || gi > 2)
+        return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden %u / inter %u must be <= 8192", who, a.hidden, a.inter);
+    if (gh == 1 && gi == 1) {
+        int rc = fm_launch_eager(a, lh, li, st);
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
     }
-#undef FM_A_CASE
-    int rc = fm_check_launch("fm_decode_gateup_kernel");
-    if (rc) return rc;
-
-    const uint32_t rbb = FM_B_NP * (64u / li);
-    dim3 gb((a.hidden + rbb - 1) / rbb), bb(64 * (a.S < 16 ? a.S : 16));
-#define FM_B_CASE(L, G)                                                        \
-    if (li == L && gi == G) {                                                  \
-        hipLaunchKernelGGL((fm_decode_down_kernel<L, G>), gb, bb, 0, st, a);  \
-    } else
-    FM_B_CASE(16, 1) FM_B_CASE(32, 1) FM_B_CASE(64, 1) FM_B_CASE(64, 2) FM_B_CASE(64, 4) {
-        return fm_fail(FM_ERR_UNSUPPORTED, "%s: no down kernel", who);
-    }
-#undef FM_B_CASE
-    return fm_check_launch("fm_decode_down_kernel");
+    const int ch = lh * 10 + gh, ci = li * 10 + gi;
+#define FM_F(A, B, C, D) \
+    if (ch == A * 10 + B && ci == C * 10 + D) return fm_launch_fused<A, B, C, D>(a, st);
+#define FM_FI(A, B) FM_F(A, B, 16, 1) FM_F(A, B, 32, 1) FM_F(A, B, 64, 1) FM_F(A, B, 64, 2)
+    FM_FI(16, 1) FM_FI(32, 1) FM_FI(64, 1) FM_FI(64, 2)
+#undef FM_FI
+#undef FM_F
+    return fm_fail(FM_ERR_UNSUPPORTED, "%s: no kernel instance for hidden %u / inter %u", who, a.hidden, a.inter);
 }
 
 extern "C" int fm_moe_decode(int K, const fm_expert_weights *experts, const int *bits,

@@ -3,13 +3,15 @@
 // Dequant arithmetic.  The reference computes, per row,
 //   sum_g sum_{i in g} (code_i * s_g + b_g) * x_i          (cpu_kernels.h:199-232)
 // which equals  sum_g ( s_g * sum_{i in g} code_i x_i  +  b_g * sum_{i in g} x_i ).
-// The kernels use the second form: codes are exact small integers, so the
-// inner dot runs on v_dot2_f32_f16 (two fp16 products, fp32 accumulate) with
-// codes unpacked by the fp16 "magic exponent" trick (OR the nibbles into the
-// mantissa of 1024.0h, then one packed fp16 FMA makes them exact integers),
-// and the per-group scale/bias are applied once per group in fp32.
-// That is ~1.6 VALU ops per 4-bit code instead of ~3 for cvt+fma, which is
-// what keeps an HBM-rate matvec under the CU's vector issue budget.
+// The kernels use the second form.  Codes are small integers, so the inner dot
+// runs on v_dot2_f32_f16 (two fp16 products, fp32 accumulate) fed straight
+// from the packed word: a nibble masked in place, with the fp16 exponent field
+// left at zero, IS the fp16 subnormal code * 2^-24 (or * 2^-20 for the nibble
+// at bits 4..7) -- exact, no conversion instruction at all.  The 2^-24 is
+// folded into the group scale and the 2^4 factors into the fp16 copy of x.
+// Per 4-bit word (8 codes): one shift, four ANDs, four dot2 = 1.1 VALU ops per
+// code, which keeps an HBM-rate stream under the CU's vector issue budget.
+// (fp16 denormals are preserved: the kernels run with denorm mode 16/64 = 3.)
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -42,26 +44,11 @@ FM_DEV fm_h2 fm_pack_h2(float lo, float hi) {
 
 FM_DEV float fm_dot2(fm_h2 a, fm_h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
-// (1024 + m*c) -> c exactly, for a code field whose lowest bit sits at mantissa
-// bit log2(m).  One v_pk_add_f16 (m == 1) or v_pk_fma_f16.
-template <int M>
-FM_DEV fm_h2 fm_magic_norm(uint32_t masked) {
-    fm_h2 v = fm_as_h2(masked | 0x64006400u);
-    if constexpr (M == 1) {
-        const fm_h2 off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-        return v + off;
-    } else {
-        const fm_h2 sc = {(_Float16)(1.0f / M), (_Float16)(1.0f / M)};
-        const fm_h2 off = {(_Float16)(-1024.0f / M), (_Float16)(-1024.0f / M)};
-        return __builtin_elementwise_fma(v, sc, off);
-    }
-}
-
 // ---- x layout per group --------------------------------------------------
 // A lane owns whole 64-element groups.  For one group it keeps 32 fp16 pairs
-// ordered to match the code pairs the unpack produces:
-//  4-bit word p (elements 8p..8p+7): pairs (x0,x4) (x1,x5) (x2,x6) (x3,x7)
-//  2-bit word p (elements 16p..16p+15): pairs (x_n, x_{n+8}), n = 0..7
+// ordered (and pre-scaled by 2^-log2(m)) to match the code pairs:
+//  4-bit word p (elements 8p..8p+7):  (x0,x4) (x1,x5)/16 (x2,x6) (x3,x7)/16
+//  2-bit word p (elements 16p..+15):  (x_n, x_{n+8}) / 4^(n mod 5 ... see fm_dot_word2)
 // plus the fp32 group sum for the bias term.
 struct FmXGroup {
     fm_h2 q[32];
@@ -77,26 +64,28 @@ FM_DEV void fm_load_xgroup(const float *__restrict__ xg, FmXGroup &g) {
             fm_f4 a = *(const fm_f4 *)(xg + 8 * p);
             fm_f4 b = *(const fm_f4 *)(xg + 8 * p + 4);
             g.q[4 * p + 0] = fm_pack_h2(a.x, b.x);
-            g.q[4 * p + 1] = fm_pack_h2(a.y, b.y);
+            g.q[4 * p + 1] = fm_pack_h2(a.y * 0.0625f, b.y * 0.0625f);
             g.q[4 * p + 2] = fm_pack_h2(a.z, b.z);
-            g.q[4 * p + 3] = fm_pack_h2(a.w, b.w);
+            g.q[4 * p + 3] = fm_pack_h2(a.w * 0.0625f, b.w * 0.0625f);
             s += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
         }
     } else {
+        // code field n of a 2-bit word sits at bit 2n (n <= 4) or 2(n-5) after >> 10
+        const float m[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             fm_f4 a0 = *(const fm_f4 *)(xg + 16 * p);
             fm_f4 a1 = *(const fm_f4 *)(xg + 16 * p + 4);
             fm_f4 b0 = *(const fm_f4 *)(xg + 16 * p + 8);
             fm_f4 b1 = *(const fm_f4 *)(xg + 16 * p + 12);
-            g.q[8 * p + 0] = fm_pack_h2(a0.x, b0.x);
-            g.q[8 * p + 1] = fm_pack_h2(a0.y, b0.y);
-            g.q[8 * p + 2] = fm_pack_h2(a0.z, b0.z);
-            g.q[8 * p + 3] = fm_pack_h2(a0.w, b0.w);
-            g.q[8 * p + 4] = fm_pack_h2(a1.x, b1.x);
-            g.q[8 * p + 5] = fm_pack_h2(a1.y, b1.y);
-            g.q[8 * p + 6] = fm_pack_h2(a1.z, b1.z);
-            g.q[8 * p + 7] = fm_pack_h2(a1.w, b1.w);
+            g.q[8 * p + 0] = fm_pack_h2(a0.x * m[0], b0.x * m[0]);
+            g.q[8 * p + 1] = fm_pack_h2(a0.y * m[1], b0.y * m[1]);
+            g.q[8 * p + 2] = fm_pack_h2(a0.z * m[2], b0.z * m[2]);
+            g.q[8 * p + 3] = fm_pack_h2(a0.w * m[3], b0.w * m[3]);
+            g.q[8 * p + 4] = fm_pack_h2(a1.x * m[4], b1.x * m[4]);
+            g.q[8 * p + 5] = fm_pack_h2(a1.y * m[5], b1.y * m[5]);
+            g.q[8 * p + 6] = fm_pack_h2(a1.z * m[6], b1.z * m[6]);
+            g.q[8 * p + 7] = fm_pack_h2(a1.w * m[7], b1.w * m[7]);
             s += ((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w)) +
                  ((b0.x + b0.y) + (b0.z + b0.w)) + ((b1.x + b1.y) + (b1.z + b1.w));
         }
@@ -104,27 +93,27 @@ FM_DEV void fm_load_xgroup(const float *__restrict__ xg, FmXGroup &g) {
     g.sum = s;
 }
 
-// sum over one group of code_i * x_i, for one 4-bit word (8 codes).
+// sum over one 4-bit word of code_i * x_i * 2^-24 (8 codes, 9 VALU ops).
 FM_DEV float fm_dot_word4(uint32_t w, const fm_h2 *q, float acc) {
     uint32_t t = w >> 8;
-    acc = fm_dot2(fm_magic_norm<1>(w & 0x000F000Fu), q[0], acc);
-    acc = fm_dot2(fm_magic_norm<16>(w & 0x00F000F0u), q[1], acc);
-    acc = fm_dot2(fm_magic_norm<1>(t & 0x000F000Fu), q[2], acc);
-    acc = fm_dot2(fm_magic_norm<16>(t & 0x00F000F0u), q[3], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x000F000Fu), q[0], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x00F000F0u), q[1], acc);
+    acc = fm_dot2(fm_as_h2(t & 0x000F000Fu), q[2], acc);
+    acc = fm_dot2(fm_as_h2(t & 0x00F000F0u), q[3], acc);
     return acc;
 }
 
-// one 2-bit word (16 codes): pairs (c_n, c_{n+8}).
+// one 2-bit word (16 codes): pairs (c_n, c_{n+8}), times 2^-24.
 FM_DEV float fm_dot_word2(uint32_t w, const fm_h2 *q, float acc) {
     uint32_t t = w >> 10;
-    acc = fm_dot2(fm_magic_norm<1>(w & 0x00030003u), q[0], acc);
-    acc = fm_dot2(fm_magic_norm<4>(w & 0x000C000Cu), q[1], acc);
-    acc = fm_dot2(fm_magic_norm<16>(w & 0x00300030u), q[2], acc);
-    acc = fm_dot2(fm_magic_norm<64>(w & 0x00C000C0u), q[3], acc);
-    acc = fm_dot2(fm_magic_norm<256>(w & 0x03000300u), q[4], acc);
-    acc = fm_dot2(fm_magic_norm<1>(t & 0x00030003u), q[5], acc);
-    acc = fm_dot2(fm_magic_norm<4>(t & 0x000C000Cu), q[6], acc);
-    acc = fm_dot2(fm_magic_norm<16>(t & 0x00300030u), q[7], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x00030003u), q[0], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x000C000Cu), q[1], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x00300030u), q[2], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x00C000C0u), q[3], acc);
+    acc = fm_dot2(fm_as_h2(w & 0x03000300u), q[4], acc);
+    acc = fm_dot2(fm_as_h2(t & 0x00030003u), q[5], acc);
+    acc = fm_dot2(fm_as_h2(t & 0x000C000Cu), q[6], acc);
+    acc = fm_dot2(fm_as_h2(t & 0x00300030u), q[7], acc);
     return acc;
 }
 
@@ -133,13 +122,23 @@ struct FmWGroup {
     fm_u4 a, b;
 };
 
+// Global-address-space loads.  Pointers that pass through LDS (staged slot
+// descriptors) lose their address space; a flat load would then share the LDS
+// wait counter, so every LDS access or cross-lane op would wait for all
+// in-flight weight prefetches.  These force global_load_* instead.
+#define FM_GLOBAL __attribute__((address_space(1)))
+FM_DEV fm_u4 fm_ldg_u4_nt(const void *p) { return __builtin_nontemporal_load((const FM_GLOBAL fm_u4 *)p); }
+FM_DEV uint16_t fm_ldg_u16(const void *p) { return *(const FM_GLOBAL uint16_t *)p; }
+FM_DEV float fm_ldg_f32(const void *p) { return *(const FM_GLOBAL float *)p; }
+FM_DEV fm_f4 fm_ldg_f4(const void *p) { return *(const FM_GLOBAL fm_f4 *)p; }
+
 template <int BITS>
 FM_DEV void fm_load_wgroup(const uint32_t *__restrict__ wg, FmWGroup &w) {
-    w.a = __builtin_nontemporal_load((const fm_u4 *)wg);
-    if constexpr (BITS == 4) w.b = __builtin_nontemporal_load((const fm_u4 *)wg + 1);
+    w.a = fm_ldg_u4_nt(wg);
+    if constexpr (BITS == 4) w.b = fm_ldg_u4_nt(wg + 4);
 }
 
-// s * sum(code*x) + b * sum(x) for one group.
+// s * sum(code*x) + b * sum(x) for one group (the dot carries codes * 2^-24).
 template <int BITS>
 FM_DEV float fm_group_dot(const FmWGroup &w, const FmXGroup &x, float s, float b) {
     float acc0 = 0.f, acc1 = 0.f;
@@ -158,15 +157,36 @@ FM_DEV float fm_group_dot(const FmWGroup &w, const FmXGroup &x, float s, float b
         acc0 = fm_dot_word2(w.a.z, &x.q[16], acc0);
         acc1 = fm_dot_word2(w.a.w, &x.q[24], acc1);
     }
-    return __builtin_fmaf(s, acc0 + acc1, b * x.sum);
+    return __builtin_fmaf(s * 16777216.0f, acc0 + acc1, b * x.sum);  // codes carried * 2^-24
 }
 
-// Sum over aligned groups of L lanes (L in {16, 32, 64}); every lane of the
-// group receives the total.
+// DPP lane moves (GFX9 encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+// row_ror:4 = 0x124, row_ror:8 = 0x128, wave_shl:1 = 0x130.
+template <int CTRL>
+FM_DEV int fm_dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+FM_DEV float fm_dpp_f(float v) { return __int_as_float(fm_dpp_i<CTRL>(__float_as_int(v))); }
+
+// Sum over aligned segments of L lanes (L in {16, 32, 64}).  The total is
+// valid in the FIRST lane of each segment (for L == 16: in every lane).
+// In-row steps are DPP adds; the cross-row steps are v_readlane into SGPRs,
+// so no LDS crossbar (ds_bpermute / ds_swizzle) round trips are involved.
 template <int L>
 FM_DEV float fm_lane_sum(float v) {
-#pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    v += fm_dpp_f<0xB1>(v);
+    v += fm_dpp_f<0x4E>(v);
+    v += fm_dpp_f<0x124>(v);
+    v += fm_dpp_f<0x128>(v);
+    if constexpr (L == 32) {
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+        v += (threadIdx.x & 32) ? r3 : r1;
+    } else if constexpr (L == 64) {
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+        const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+        v = (v + r1) + (r2 + r3);
+    }
     return v;
 }
 

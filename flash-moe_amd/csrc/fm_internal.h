@@ -38,3 +38,6 @@ static inline int fm_pick_lanes(uint32_t groups, int *lpr, int *gpl) {
 // Validation shared by launchers: returns FM_OK or an FM_ERR_* (message set).
 int fm_check_dims(const char *who, uint32_t out_dim, uint32_t in_dim, uint32_t group_size,
                   int bits);
+
+// Compute units of the current device (cached per device).
+int fm_num_cus(void);

@@ -61,8 +61,8 @@ __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__re
             uint32_t g = gl + j * LPR;
             if (row < sp.out_dim && g < G) {
                 fm_load_wgroup<BITS>(sp.W + (size_t)row * wpr + g * WPG, wv[p][j]);
-                sv[p][j] = fm_bf16_to_f32(sp.s[(size_t)row * G + g]);
-                bv[p][j] = fm_bf16_to_f32(sp.b[(size_t)row * G + g]);
+                sv[p][j] = fm_bf16_to_f32(fm_ldg_u16(sp.s + (size_t)row * G + g));
+                bv[p][j] = fm_bf16_to_f32(fm_ldg_u16(sp.b + (size_t)row * G + g));
             }
         }
     }

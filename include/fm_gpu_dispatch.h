@@ -120,7 +120,11 @@ int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *
 /* ------------------------------------------------------------------------ */
 
 /* Workspace bytes for fm_moe_decode / fm_moe_decode_pool /
- * fm_encode_experts_batched with n_slots = K (+1 if a shared expert). */
+ * fm_encode_experts_batched with n_slots = K (+1 if a shared expert).
+ * The workspace holds a small control block of counters: it must be
+ * zero-filled (e.g. hipMemset) before its first use and 256-byte aligned;
+ * every call leaves the counters at zero again.  Calls that share one
+ * workspace must be ordered (same stream); concurrent calls need their own. */
 size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
 
 /* K expert FFNs sharing input x, one output per expert:

@@ -98,7 +98,7 @@ def test_moe_decode_host_routed(orc, dev, K, bitmode, hidden, inter):
     blobs, x, hm, w, score = _decode_inputs(K + hidden // 512, K, bl, hidden, inter)
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, bl[i], hidden, inter) for i, db in enumerate(dblobs)]
-    ws = torch.empty(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
     out = torch.empty(hidden, dtype=torch.float32, device=dev)
     ob = torch.empty(hidden, dtype=torch.int16, device=dev)
     fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, hidden, inter, shared=ex[K], shared_bits=bl[K],
@@ -121,7 +121,7 @@ def test_moe_decode_valid_mask_and_no_shared(orc, dev):
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, 4, HIDDEN, INTER) for db in dblobs]
     valid = [1, 0, 1, 1, 0, 1]
-    ws = torch.empty(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, valid=valid)
     torch.cuda.synchronize()
@@ -137,7 +137,7 @@ def test_encode_experts_batched_and_combine(orc, dev):
     blobs, x, hm, w, score = _decode_inputs(12, K, bl)
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
-    ws = torch.empty(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
     eo = torch.zeros((K + 1, HIDDEN), dtype=torch.float32, device=dev)
     fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
     torch.cuda.synchronize()
@@ -179,7 +179,7 @@ def test_moe_decode_pool_device_routing(orc, dev, pool64):
     idx = torch.empty((1, K), dtype=torch.int32, device=dev)
     w = torch.empty((1, K), dtype=torch.float32, device=dev)
     fm.route_topk(T(lg, dev), K, idx, w)
-    ws = torch.empty(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode_pool(pool, idx, w, T(x, dev), out, ws, shared=sh, shared_bits=4,
                        shared_score=T(np.array([g]), dev), h_mid=T(hm, dev))
@@ -214,7 +214,7 @@ def test_moe_forward_layer(orc, dev, pool64):
     L.shared_bits = 4
     L.has_shared = 1
     L.pool = pool.c
-    ws = torch.empty(fm.moe_forward_workspace_bytes(L, K), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(fm.moe_forward_workspace_bytes(L, K), dtype=torch.uint8, device=dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_forward(L, K, T(hp, dev), T(hm, dev), out, ws)
     torch.cuda.synchronize()
