@@ -51,6 +51,7 @@ def bench_decode(args, dev):
     from fmoe_amd import synth
 
     pool, sample_blobs, _ = make_pool(lambda e: 4, 3000)
+    args._pool = pool
     rng = synth.rng_for(3001)
     n_sh = 16
     shared_blobs = [synth.expert_blob((3002, i), H, I, 4) for i in range(n_sh)]
@@ -111,6 +112,55 @@ def bench_decode(args, dev):
     return res, sample_blobs
 
 
+def bench_prefill(args, dev, pool):
+    """Config 3: 512 tokens, 512 experts, top-10 over Zipf(1.1) logits + shared
+    expert, one MoE layer = routing + grouped expert GEMMs + combine."""
+    import numpy as np
+    import torch
+    import fmoe_amd as fm
+    from fmoe_amd import synth
+    Tn = 512
+    rng = synth.rng_for(3101)
+    n = args.prefill_warmup + args.prefill_steps
+    logits = [torch.from_numpy(synth.zipf_logits(rng, Tn, E)).to(dev) for _ in range(n)]
+    X = torch.from_numpy(synth.hidden_vec(rng, H, (Tn, H))).to(dev)
+    hm = torch.from_numpy(rng.normal(0, 1, (Tn, H)).astype(np.float32)).to(dev)
+    g = torch.from_numpy(rng.normal(0, 1, Tn).astype(np.float32)).to(dev)
+    sh_blob = torch.from_numpy(synth.expert_blob((3102, 0), H, I, 4)).to(dev)
+    sh = fm.experts_from_blob(sh_blob, 4, H, I)
+    idx = torch.empty((Tn, K), dtype=torch.int32, device=dev)
+    w = torch.empty((Tn, K), dtype=torch.float32, device=dev)
+    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    out = torch.empty((Tn, H), dtype=torch.float32, device=dev)
+    ob = torch.empty((Tn, H), dtype=torch.int16, device=dev)
+
+    def step(i):
+        fm.route_topk(logits[i], K, idx, w)
+        fm.prefill_moe(pool, idx, w, X, out, ws, shared=sh, shared_bits=4, shared_scores=g, h_mid=hm, out_bf16=ob)
+
+    uniq = []
+    for i in range(args.prefill_warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.prefill_warmup, n):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.prefill_steps
+    for i in range(args.prefill_warmup, n):
+        fm.route_topk(logits[i], K, idx, w)
+        uniq.append(len(np.unique(idx.cpu().numpy())))
+    blob = fm.layout_of(H, I, 64, 4).size
+    bytes_step = (float(np.mean(uniq)) + 1) * blob + Tn * H * 4 * 3 + Tn * H * 2
+    flops = (Tn * K + Tn) * 3 * 2 * H * I
+    return {"ms": ms, "tokens_per_s": Tn / (ms * 1e-3), "unique_experts": float(np.mean(uniq)),
+            "hbm_gbs": bytes_step / (ms * 1e-3) / 1e9, "hbm_frac": bytes_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "tflops": flops / (ms * 1e-3) / 1e12, "mfma_frac": flops / (ms * 1e-3) / 2.5e15,
+            "bytes_per_step": bytes_step, "flops_per_step": flops}
+
+
 def cpu_baseline(sample_blobs, budget_s=10.0):
     """The reference's own CPU kernels (oracle/_ref: cpu_dequant_matvec +
     cpu_swiglu + cpu_vec_madd, one core) on config-2 steps until ~budget_s."""
@@ -165,6 +215,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--prefill-warmup", type=int, default=2)
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
@@ -177,6 +230,10 @@ def main():
     dec, sample = bench_decode(args, dev)
     log(f"decode: {dec['step_ms'] * 1e3:.2f} us/step, {dec['value']:.0f} GB/s; fused launch "
         f"{dec['roofline']['kernel_us']:.2f} us = {dec['roofline']['achieved']:.0f} GB/s")
+    pre = None if args.no_prefill else bench_prefill(args, dev, args._pool)
+    if pre:
+        log(f"prefill: {pre['ms']:.3f} ms/layer, {pre['tokens_per_s']:.0f} tok/s, {pre['hbm_gbs']:.0f} GB/s, "
+            f"{pre['tflops']:.1f} TFLOP/s")
     cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_budget)
     line = {
         "metric": "4-bit expert FFN decode GB/s (% of HBM peak); prefill MoE-layer tokens/s",
@@ -188,6 +245,11 @@ def main():
                                "4096->1024->4096 SwiGLU, 4-bit g64, device routing",
                    "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"]},
         "roofline": dec["roofline"],
+        "prefill": None if pre is None else {
+            "workload": "config 3: 512 tokens, 512 experts, top-10 Zipf(1.1) + shared, grouped MFMA dequant-GEMM",
+            "tokens_per_s": round(pre["tokens_per_s"]), "ms_per_layer": pre["ms"],
+            "unique_experts": pre["unique_experts"], "hbm_gbs": round(pre["hbm_gbs"], 1),
+            "hbm_frac": pre["hbm_frac"], "tflops": round(pre["tflops"], 2), "mfma_frac": pre["mfma_frac"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
