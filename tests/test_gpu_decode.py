@@ -55,13 +55,19 @@ def test_batch_matvec_mixed(orc, dev):
 
 @pytest.mark.parametrize("Tn,E,K,kind", [(1, 512, 10, "normal"), (512, 512, 10, "zipf"), (64, 512, 1, "normal"),
                                          (16, 64, 64, "normal"), (8, 10, 10, "normal"), (32, 128, 16, "dup"),
-                                         (4, 4096, 8, "normal"), (3, 512, 20, "normal")])
+                                         (4, 4096, 8, "normal"), (3, 512, 20, "normal"),
+                                         (64, 512, 10, "normal"), (4, 512, 10, "asc"), (4, 300, 16, "asc"),
+                                         (4, 512, 10, "desc"), (8, 4096, 64, "normal"), (16, 70, 7, "dup")])
 def test_route_topk(orc, dev, Tn, E, K, kind):
     import torch
     say("route", Tn, E, K, kind)
     rng = synth.rng_for(5, Tn, E, K)
     if kind == "zipf":
         lg = synth.zipf_logits(rng, Tn, E)
+    elif kind in ("asc", "desc"):
+        # ascending: every element is inserted (long eviction chains / overflow path); descending: none
+        lg = np.sort(rng.normal(0, 1, (Tn, E)), axis=1).astype(np.float32)
+        lg = lg if kind == "asc" else np.ascontiguousarray(lg[:, ::-1])
     elif kind == "dup":
         lg = np.round(rng.normal(0, 1, (Tn, E)), 1).astype(np.float32)
     else:
