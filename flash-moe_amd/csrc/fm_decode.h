@@ -1,0 +1,93 @@
+// fm_decode.h -- definitions shared by the decode-step kernels: slot
+// descriptors, launch arguments and the epoch-tagged cross-wave hand-off.
+#pragma once
+#include "fm_device.h"
+#include "fm_internal.h"
+
+#define FM_MAX_SLOTS (FM_MAX_K + 1)
+
+struct FmSlot {
+    const uint32_t *gw, *uw, *dw;
+    const uint16_t *gs, *gb, *us, *ub, *ds, *db;
+    float weight;
+    int bits;
+    int valid;
+    int pad;
+};
+
+struct FmDecodeArgs {
+    FmSlot slot[FM_MAX_SLOTS];
+    int S;          // slots in use (K routed + optional shared)
+    int K;          // routed slots
+    int has_shared; // slot K is the shared expert
+    int pool_mode;  // routed slots resolved from pool + idx on the device
+    int mode;       // 0: combine into out; 1: per-slot outputs (expert_out)
+    int pad0;
+    const void *const *pool_blobs;
+    const uint8_t *pool_bits;
+    const int *idx;
+    const float *wdev;
+    uint64_t off4[9], off2[9];
+    uint32_t pool_n;
+    uint32_t hidden, inter;
+    float shared_w_host;       // used when shared_score == NULL and host mode
+    const float *shared_score; // device scalar (pre-sigmoid) or NULL
+    const float *x;
+    const float *h_mid;
+    float *out;
+    uint16_t *out_bf16;
+    float *expert_out;
+    uint64_t *act2;  // [S][inter]  (value bits | epoch << 32) SwiGLU activations
+    uint64_t *y2;    // [S][hidden] (value bits | epoch << 32) per-slot down outputs
+    uint32_t *err;   // set when a bounded wait gave up
+    uint32_t epoch;  // this call's tag (never 0)
+    int phases;      // mfma kernel: bit 0 gate/up, bit 1 down+combine (0 = both)
+};
+
+__device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
+    if (!a.pool_mode || k >= a.K) return a.slot[k];
+    FmSlot s;
+    int e = a.idx[k];
+    if (e < 0 || (uint32_t)e >= a.pool_n) {
+        s.valid = 0;
+        s.bits = 4;
+        s.weight = 0.f;
+        return s;
+    }
+    const char *blob = (const char *)a.pool_blobs[e];
+    int bits = a.pool_bits[e];
+    const uint64_t *off = bits == 2 ? a.off2 : a.off4;
+    s.gw = (const uint32_t *)(blob + off[0]);
+    s.gs = (const uint16_t *)(blob + off[1]);
+    s.gb = (const uint16_t *)(blob + off[2]);
+    s.uw = (const uint32_t *)(blob + off[3]);
+    s.us = (const uint16_t *)(blob + off[4]);
+    s.ub = (const uint16_t *)(blob + off[5]);
+    s.dw = (const uint32_t *)(blob + off[6]);
+    s.ds = (const uint16_t *)(blob + off[7]);
+    s.db = (const uint16_t *)(blob + off[8]);
+    s.bits = bits;
+    s.weight = a.wdev[k];
+    s.valid = blob != nullptr && (bits == 2 || bits == 4);
+    return s;
+}
+
+// Cross-wave hand-off without atomics read-modify-writes or cache
+// maintenance.  Every handed-off value is stored together with this call's
+// epoch as ONE 64-bit agent-coherent store (global_store_dwordx2 sc1); a
+// consumer polls the 64-bit words it needs with agent-coherent loads until
+// every tag equals the epoch.  No counters (which would serialise thousands of
+// device-scope atomics on one cache line), no L2 write-back/invalidate, and no
+// reset: a new call simply uses a new epoch.
+__device__ __forceinline__ void fm_put_tagged(uint64_t *p, float v, uint32_t epoch) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+#define FM_SPIN_MAX (1u << 16)
+
+// Alternative launchers tried by fm_decode_launch before the eager kernel;
+// each returns FM_ERR_UNSUPPORTED (message cleared by the caller) when the
+// shape or slot mix is outside what it implements.
+int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st);

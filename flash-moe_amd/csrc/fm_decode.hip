@@ -20,93 +20,12 @@
 //
 // Slots are described either on the host (kernel arguments) or, in pool mode,
 // resolved on the device from routing indices (no host round trip).
-#include "fm_device.h"
-#include "fm_internal.h"
+#include "fm_decode.h"
 
 #include <atomic>
 
-#define FM_MAX_SLOTS (FM_MAX_K + 1)
 #define FM_DECODE_BLOCKS_PER_CU 4  // persistent 256-thread blocks per CU (cap)
 
-struct FmSlot {
-    const uint32_t *gw, *uw, *dw;
-    const uint16_t *gs, *gb, *us, *ub, *ds, *db;
-    float weight;
-    int bits;
-    int valid;
-    int pad;
-};
-
-struct FmDecodeArgs {
-    FmSlot slot[FM_MAX_SLOTS];
-    int S;          // slots in use (K routed + optional shared)
-    int K;          // routed slots
-    int has_shared; // slot K is the shared expert
-    int pool_mode;  // routed slots resolved from pool + idx on the device
-    int mode;       // 0: combine into out; 1: per-slot outputs (expert_out)
-    int pad0;
-    const void *const *pool_blobs;
-    const uint8_t *pool_bits;
-    const int *idx;
-    const float *wdev;
-    uint64_t off4[9], off2[9];
-    uint32_t pool_n;
-    uint32_t hidden, inter;
-    float shared_w_host;       // used when shared_score == NULL and host mode
-    const float *shared_score; // device scalar (pre-sigmoid) or NULL
-    const float *x;
-    const float *h_mid;
-    float *out;
-    uint16_t *out_bf16;
-    float *expert_out;
-    uint64_t *act2;  // [S][inter]  (value bits | epoch << 32) SwiGLU activations
-    uint64_t *y2;    // [S][hidden] (value bits | epoch << 32) per-slot down outputs
-    uint32_t *err;   // set when a bounded wait gave up
-    uint32_t epoch;  // this call's tag (never 0)
-};
-
-__device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
-    if (!a.pool_mode || k >= a.K) return a.slot[k];
-    FmSlot s;
-    int e = a.idx[k];
-    if (e < 0 || (uint32_t)e >= a.pool_n) {
-        s.valid = 0;
-        s.bits = 4;
-        s.weight = 0.f;
-        return s;
-    }
-    const char *blob = (const char *)a.pool_blobs[e];
-    int bits = a.pool_bits[e];
-    const uint64_t *off = bits == 2 ? a.off2 : a.off4;
-    s.gw = (const uint32_t *)(blob + off[0]);
-    s.gs = (const uint16_t *)(blob + off[1]);
-    s.gb = (const uint16_t *)(blob + off[2]);
-    s.uw = (const uint32_t *)(blob + off[3]);
-    s.us = (const uint16_t *)(blob + off[4]);
-    s.ub = (const uint16_t *)(blob + off[5]);
-    s.dw = (const uint32_t *)(blob + off[6]);
-    s.ds = (const uint16_t *)(blob + off[7]);
-    s.db = (const uint16_t *)(blob + off[8]);
-    s.bits = bits;
-    s.weight = a.wdev[k];
-    s.valid = blob != nullptr && (bits == 2 || bits == 4);
-    return s;
-}
-
-// Cross-wave hand-off without atomics read-modify-writes or cache
-// maintenance.  Every handed-off value is stored together with this call's
-// epoch as ONE 64-bit agent-coherent store (global_store_dwordx2 sc1); a
-// consumer polls the 64-bit words it needs with agent-coherent loads until
-// every tag equals the epoch.  No counters (which would serialise thousands of
-// device-scope atomics on one cache line), no L2 write-back/invalidate, and no
-// reset: a new call simply uses a new epoch.
-__device__ __forceinline__ void fm_put_tagged(uint64_t *p, float v, uint32_t epoch) {
-    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-#define FM_SPIN_MAX (1u << 16)
 
 // ---------------------------------------------------------------- phase A --
 // Persistent stream over the (slot, row-pass) units of every expert's gate and
@@ -390,6 +309,9 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
 // then follows the data in issue order.  Between the phases the block stages
 // the activations of its (at most two) down-projection slots once in LDS.
 #define FM_UMAX 6
+#ifndef FM_DX_MARK
+#define FM_DX_MARK(n)
+#endif
 
 struct FmUnitW {
     FmWGroup w;
@@ -501,6 +423,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
     const uint64_t NB = (uint64_t)a.S * upsB;
     const uint32_t v0 = (uint32_t)(NB * w / nwaves), v1 = (uint32_t)(NB * (w + 1) / nwaves);
 
+    FM_DX_MARK(0);
     // ---- issue every weight load of this wave ----
     FmUnitW ga[FM_UMAX], ua[FM_UMAX];
 #pragma unroll
@@ -515,6 +438,8 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
             fm_unit_load(s.uw, s.us, s.ub, s.bits, row, a.hidden, glA, ok, ua[i]);
         }
     }
+    FmUnitW db[FM_UMAX];
+    FM_DX_MARK(1);
     // ---- A: gate/up + SwiGLU -> tagged act ----
     FmXGroup xg;
     int xbits = 0;
@@ -544,12 +469,8 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                 if (glA == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)k * a.inter + row], fm_silu_mul(pg, pu), a.epoch);
             }
         }
-    }
-
-    // ---- issue the down-projection weight loads (independent of act) ----
-    FmUnitW db[FM_UMAX];
-#pragma unroll
-    for (int i = 0; i < FM_UMAX; i++) {
+        // issue down-projection unit i's loads (independent of act) between
+        // gate/up computations, so the memory queue stays full while computing
         const uint32_t v = v0 + i;
         if (v < v1) {
             const int k = v / upsB;
@@ -560,6 +481,8 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
         }
     }
 
+    FM_DX_MARK(2);
+    FM_DX_MARK(3);
     // ---- stage the block's down-projection slots' activations ----
     const uint32_t bv0 = (uint32_t)(NB * (blockIdx.x * 4) / nwaves);
     const uint32_t bv1 = (uint32_t)(NB * (blockIdx.x * 4 + 4) / nwaves);
@@ -602,6 +525,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
     }
     __syncthreads();
 
+    FM_DX_MARK(4);
     // ---- B: down projection -> tagged y (or per-slot outputs) ----
     const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
     float *stage = stage_all + wv * (FM_UMAX * a.S * RPPB);
@@ -635,6 +559,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
         }
     }
 
+    FM_DX_MARK(5);
     // ---- combine the passes whose last slot this wave computed ----
     if (a.mode == 0) {
         // units [v0, v1) of the last slot -> passes; gather other slots' y for
@@ -705,6 +630,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
             }
         }
     }
+    FM_DX_MARK(6);
 }
 
 // ---------------------------------------------------------------- combine --
@@ -833,6 +759,11 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     int lh, gh, li, gi;
     if (!fm_pick_lanes(a.hidden / 64, &lh, &gh) || !fm_pick_lanes(a.inter / 64, &li, &gi) || gh > 2 || gi > 2)
         return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden %u / inter %u must be <= 8192", who, a.hidden, a.inter);
+    {
+        int rc = fm_launch_decode_mfma(a, st);
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
+    }
     if (gh == 1 && gi == 1) {
         int rc = fm_launch_eager(a, lh, li, st);
         if (rc != FM_ERR_UNSUPPORTED) return rc;

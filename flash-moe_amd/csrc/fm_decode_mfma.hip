@@ -1,0 +1,437 @@
+// fm_decode_mfma.hip -- the decode step (K routed experts + shared expert) with
+// every expert dot product on the matrix cores.
+//
+// Same contract as the eager kernel in fm_decode.hip (CMD3 of
+// layer_forward.h:3895-3993: gate/up, SwiGLU, down, weighted combine into the
+// residual, one launch), restructured so the packed codes feed
+// v_mfma_f32_16x16x32_f16 directly:
+//
+//  * codes are the B operand (one row per lane column): a masked nibble with a
+//    zero fp16 exponent field IS the subnormal code*2^-24 (code*2^-20 for the
+//    field at bits 4-7), so one shift and four ANDs turn a packed word into
+//    the operand (no conversion, no dot instructions);
+//  * the input vector is the A operand, but only in the operand row m that
+//    equals the group index mod 16 -- every other row is zero.  D[m][row] thus
+//    accumulates, over 32 MFMAs, the 16 per-group dot products of 16 weight
+//    rows separately, and the per-(row, group) scale/bias fold happens once per
+//    16 groups:  acc_row += s_g * 2^24 * D[g mod 16][row] + b_g * sum(x_g).
+//    In the D layout a lane holds four consecutive groups of one row, so the
+//    fold reads 8-byte scale/bias runs.
+//
+// Work split (one 256-thread workgroup = 4 wavefronts, all resident):
+//  A  block b < S*I/16: 16 gate/up rows of slot b/(I/16); wave w takes the
+//     w-th 1024-code quarter of the row (H = 4096); the 4 partial gate/up
+//     sums meet in LDS, the block applies SwiGLU and publishes 16 tagged
+//     activations.
+//  B  block b < S*H/64: 64 down rows of slot b/(H/64), 16 per wave, k = I.
+//     The block waits for its slot's I tagged activations, then streams.
+//  C  the blocks of the last slot also combine their 64 rows over all slots
+//     in the slot order of cpu_vec_madd (layer_forward.h:1257, 1295-1305).
+// Every wave issues all of its A and B weight loads before computing, so the
+// whole expert stream is in flight from the first microsecond.
+#include "fm_decode.h"
+
+typedef _Float16 fmm_h8 __attribute__((ext_vector_type(8)));
+typedef float fmm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
+
+#define FMM_H 4096             // hidden size this kernel is specialised for
+#define FMM_MAXI 1024          // largest intermediate size (k of the down rows)
+#define FMM_GH (FMM_H / 64)    // input groups of a gate/up row
+#define FMM_GI (FMM_MAXI / 64) // input groups of a down row (max)
+#define FMM_BLOCKS_PER_CU 3
+#ifndef FM_DX_MARK
+#define FM_DX_MARK(n)
+#endif
+
+struct __attribute__((aligned(16))) FmmLds {
+    fm_h2 xq[2][FMM_GH][32];  // x as MFMA operand rows: [4-bit | 2-bit layout][group][32 pairs]
+    fm_h2 aq[2][FMM_GI][32];  // the B slot's activations, same layouts
+    fm_h2 zero[32];           // zero operand rows (128 B)
+    float xsum[FMM_GH];       // per-group sums of x
+    float asum[FMM_GI];       // per-group sums of the activations
+    float act[FMM_MAXI];      // staged activations (fp32)
+    float part[4][16][2];     // per-wave partial gate/up sums of the A rows
+    float ylast[64];          // this block's rows of the last slot's y
+    FmSlot sd[FM_MAX_SLOTS];
+};
+
+// One packed word -> the B operand of one MFMA (8 subnormal fp16 codes).
+// 4-bit: [c0 c4 c1' c5' c2 c6 c3' c7'] (' = field *16); 2-bit: half h of the
+// word's 16 codes, pairs n = 4h..4h+3 of the fm_dot_word2 layout.
+template <int BITS>
+FM_DEV fmm_h8 fmm_codes(uint32_t w, int h) {
+    uint32_t r0, r1, r2, r3;
+    if constexpr (BITS == 4) {
+        const uint32_t t = w >> 8;
+        r0 = w & 0x000F000Fu;
+        r1 = w & 0x00F000F0u;
+        r2 = t & 0x000F000Fu;
+        r3 = t & 0x00F000F0u;
+    } else if (h == 0) {
+        r0 = w & 0x00030003u;
+        r1 = w & 0x000C000Cu;
+        r2 = w & 0x00300030u;
+        r3 = w & 0x00C000C0u;
+    } else {
+        const uint32_t t = w >> 10;
+        r0 = w & 0x03000300u;
+        r1 = t & 0x00030003u;
+        r2 = t & 0x000C000Cu;
+        r3 = t & 0x00300030u;
+    }
+    fm_u4 v = {r0, r1, r2, r3};
+    return __builtin_bit_cast(fmm_h8, v);
+}
+
+FM_DEV fmm_h8 fmm_lds_op(const fm_h2 *p) { return __builtin_bit_cast(fmm_h8, *(const fm_u4 *)p); }
+
+// One 64-element group of v (fp32, in LDS) -> operand row layout for BITS,
+// 32 pairs; thread e (0..31) writes pair e.
+FM_DEV void fmm_build_pair(const float *v, int bits, int e, fm_h2 *dst) {
+    if (bits == 4) {
+        const int p = e >> 2, j = e & 3;
+        const float m = (j & 1) ? 0.0625f : 1.f;
+        dst[e] = fm_pack_h2(v[8 * p + j] * m, v[8 * p + 4 + j] * m);
+    } else {
+        const int p = e >> 3, n = e & 7;
+        // pair n: (x_n, x_{n+8}) / 4^(field position of code n in the word)
+        const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+        dst[e] = fm_pack_h2(v[16 * p + n] * mt[n], v[16 * p + 8 + n] * mt[n]);
+    }
+}
+
+// Sum over the 16 lanes of each DPP row (result valid in every lane).
+FM_DEV float fmm_row_sum(float v) {
+    v += fm_dpp_f<0xB1>(v);
+    v += fm_dpp_f<0x4E>(v);
+    v += fm_dpp_f<0x124>(v);
+    v += fm_dpp_f<0x128>(v);
+    return v;
+}
+
+// Registers of one unit: the codes a lane streams (4 chunks, 32 B per chunk
+// for 4-bit, 16 B for 2-bit) plus its 4-group scale/bias runs.
+struct FmmCodes {
+    fm_u4 c[8];
+};
+
+// Issue the loads of 16 rows x 16 groups (groups g0 .. g0+15 of each row) of
+// one matrix: lane (n = row, kq) loads group g0 + 4c + kq of row n for chunks
+// c = 0..3, and the scale/bias of groups g0 + 4q .. g0 + 4q + 3.
+FM_DEV void fmm_issue(const uint32_t *W, const uint16_t *S, const uint16_t *B, int bits, uint32_t row0,
+                      uint32_t in_dim, uint32_t g0, bool ok, FmmCodes &cd, fmm_u2 &sc, fmm_u2 &bi) {
+    if (!ok) return;
+    const int lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const uint32_t G = in_dim / 64;
+    const uint32_t row = row0 + n;
+    const uint32_t wpg = 2 * bits;  // words per group
+    const uint32_t *wr = W + (size_t)row * (G * wpg);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        // 4-bit: each load instruction covers 64 contiguous bytes of every row,
+        // half h of chunk c = words 16h + 4kq .. +3 (group 4c + 2h + kq/2);
+        // 2-bit: group 4c + kq (its 4 words)
+        const uint32_t *p = bits == 4 ? wr + (g0 + 4 * c) * 8 + 4 * kq : wr + (g0 + 4 * c + kq) * 4;
+        cd.c[2 * c] = fm_ldg_u4_nt(p);
+        if (bits == 4) cd.c[2 * c + 1] = fm_ldg_u4_nt(p + 16);
+    }
+    sc = *(const FM_GLOBAL fmm_u2 *)(S + (size_t)row * G + g0 + 4 * kq);
+    bi = *(const FM_GLOBAL fmm_u2 *)(B + (size_t)row * G + g0 + 4 * kq);
+}
+
+FM_DEV uint32_t fmm_word(const FmmCodes &cd, int c, int wi) {
+    const fm_u4 v = cd.c[2 * c + (wi >> 2)];
+    const int j = wi & 3;
+    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
+// 32 MFMAs over 16 groups: D[m][row] += x_op[m] . codes, the x operand row of
+// this lane active only for its (chunk, kq) -- see the file header.  The LDS
+// operand of step j+1 is read during step j; scheduling barriers keep the
+// compiler from hoisting further reads (registers are the scarce resource).
+template <int BITS>
+FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, fmm_f4 &d0, fmm_f4 &d1) {
+    const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+    // Operand row m carries group g0 + m.  4-bit: word i of chunk c in slot kq
+    // belongs to group 4c + 2(i/4) + kq/2 (word 4(kq%2) + i%4 of it); 2-bit:
+    // to group 4c + kq (word i/2, half i%2).
+    auto src_of = [&](int j) -> const fm_h2 * {
+        const int c = j >> 3, i = j & 7;
+        if constexpr (BITS == 4) {
+            const bool on = (kq >> 1) == (m & 1) && c == (m >> 2) && (i >> 2) == ((m >> 1) & 1);
+            return on ? xq_grp0 + 32 * m + 16 * (kq & 1) + 4 * (i & 3) : zero;
+        } else {
+            const bool on = kq == (m & 3) && c == (m >> 2);
+            return on ? xq_grp0 + 32 * m + 4 * i : zero;
+        }
+    };
+    fmm_h8 xo = fmm_lds_op(src_of(0));
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int c = j >> 3, i = j & 7;
+        fmm_h8 xn = xo;
+        if (j + 1 < 32) xn = fmm_lds_op(src_of(j + 1));
+        fmm_h8 co;
+        if constexpr (BITS == 4)
+            co = fmm_codes<4>(fmm_word(cd, c, i), 0);
+        else
+            co = fmm_codes<2>(fmm_word(cd, c, i >> 1), i & 1);
+        if (i & 1)
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d1, 0, 0, 0);
+        else
+            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d0, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        xo = xn;
+    }
+}
+
+// Fold: lane (row n, q) holds D[4q+v][n] = dot of row n with group g0+4q+v.
+FM_DEV float fmm_fold(const fmm_f4 &d, fmm_u2 sc, fmm_u2 bi, const float *gsum4) {
+    const float s0 = __uint_as_float(sc.x << 16), s1 = __uint_as_float(sc.x & 0xffff0000u);
+    const float s2 = __uint_as_float(sc.y << 16), s3 = __uint_as_float(sc.y & 0xffff0000u);
+    const float b0 = __uint_as_float(bi.x << 16), b1 = __uint_as_float(bi.x & 0xffff0000u);
+    const float b2 = __uint_as_float(bi.y << 16), b3 = __uint_as_float(bi.y & 0xffff0000u);
+    const float K24 = 16777216.0f;
+    float r = __builtin_fmaf(s0 * K24, d[0], b0 * gsum4[0]);
+    r += __builtin_fmaf(s1 * K24, d[1], b1 * gsum4[1]);
+    r += __builtin_fmaf(s2 * K24, d[2], b2 * gsum4[2]);
+    r += __builtin_fmaf(s3 * K24, d[3], b3 * gsum4[3]);
+    return r;
+}
+
+// Sum over the four lanes n, n+16, n+32, n+48 (valid in every lane).
+FM_DEV float fmm_q_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(FmDecodeArgs a) {
+    __shared__ FmmLds L;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = lane & 15, q = lane >> 4;
+    const uint32_t H = a.hidden, I = a.inter;
+    const uint32_t GI = I / 64;
+    const uint32_t tilesA = I / 16, tilesB = H / 64;
+    const uint32_t b = blockIdx.x;
+    const bool hasA = b < (uint32_t)a.S * tilesA;
+    const bool hasB = b < (uint32_t)a.S * tilesB;
+    const int kA = hasA ? (int)(b / tilesA) : 0;
+    const int kB = hasB ? (int)(b / tilesB) : 0;
+
+    if (tid < a.S) L.sd[tid] = fm_get_slot(a, tid);
+    if (tid < 32) L.zero[tid] = fm_as_h2(0u);
+    __syncthreads();
+    const FmSlot sA = L.sd[kA], sB = L.sd[kB];
+    const int ph = a.phases ? a.phases : 3;
+    const bool doA = (ph & 1) && hasA && sA.valid, doB = (ph & 2) && hasB && sB.valid;
+
+    FM_DX_MARK(0);
+    // x first: thread t holds elements 16*(t%4) .. +15 of group t/4.  Loaded
+    // before the weights, so using it later waits only for these loads.
+    fm_f4 xr[4];
+    {
+        const float *xp = a.x + 16 * tid;
+#pragma unroll
+        for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(xp + 4 * j);
+    }
+    // ---- issue every weight load of this wave ----
+    const uint32_t rowA0 = (b % tilesA) * 16;
+    FmmCodes cg, cu, cdn;
+    fmm_u2 sg = {0, 0}, bg = {0, 0}, su = {0, 0}, bu = {0, 0}, sdn = {0, 0}, bdn = {0, 0};
+    fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg);
+    fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu);
+    const uint32_t rowB0 = (b % tilesB) * 64 + 16 * wv;
+    fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn);
+
+    FM_DX_MARK(1);
+    // ---- x operand rows in both layouts, and the group sums ----
+    {
+        const int g = tid >> 2, qq = tid & 3;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[4 * j] = xr[j].x;
+            v[4 * j + 1] = xr[j].y;
+            v[4 * j + 2] = xr[j].z;
+            v[4 * j + 3] = xr[j].w;
+        }
+        // 4-bit words 2qq, 2qq+1: pair j of word p = (x_{8p+j}, x_{8p+4+j}) * (j odd ? 1/16 : 1)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float m = (j & 1) ? 0.0625f : 1.f;
+                L.xq[0][g][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+            }
+        // 2-bit word qq: pair n = (x_n, x_{n+8}) / 4^(field position of code n)
+        const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+        for (int n = 0; n < 8; n++) L.xq[1][g][8 * qq + n] = fm_pack_h2(v[n] * mt[n], v[8 + n] * mt[n]);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if (qq == 0) L.xsum[g] = s;
+    }
+    __syncthreads();
+
+    FM_DX_MARK(2);
+    // ---- A: gate/up partials of 16 rows over this wave's 16 groups ----
+    if (doA) {
+        fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
+        const fm_h2 *xq = &L.xq[sA.bits == 4 ? 0 : 1][16 * wv][0];
+        if (sA.bits == 4) {
+            fmm_mma<4>(cg, xq, L.zero, g0, g1);
+            fmm_mma<4>(cu, xq, L.zero, u0, u1);
+        } else {
+            fmm_mma<2>(cg, xq, L.zero, g0, g1);
+            fmm_mma<2>(cu, xq, L.zero, u0, u1);
+        }
+        const float *gs4 = &L.xsum[16 * wv + 4 * q];
+        float pg = fmm_fold(g0 + g1, sg, bg, gs4);
+        float pu = fmm_fold(u0 + u1, su, bu, gs4);
+        pg = fmm_q_sum(pg);
+        pu = fmm_q_sum(pu);
+        if (lane < 16) {
+            L.part[wv][n][0] = pg;
+            L.part[wv][n][1] = pu;
+        }
+    }
+    FM_DX_MARK(3);
+    __syncthreads();
+    if (doA && tid < 16) {
+        const float g = (L.part[0][tid][0] + L.part[1][tid][0]) + (L.part[2][tid][0] + L.part[3][tid][0]);
+        const float u = (L.part[0][tid][1] + L.part[1][tid][1]) + (L.part[2][tid][1] + L.part[3][tid][1]);
+        fm_put_tagged(&a.act2[(size_t)kA * I + rowA0 + tid], fm_silu_mul(g, u), a.epoch);
+    }
+
+    FM_DX_MARK(4);
+    // ---- B: stage the slot's activations, then 16 down rows per wave ----
+    if (doB) {
+        constexpr int MAXQ = FMM_MAXI / 256;
+        uint64_t t[MAXQ];
+        const uint64_t *src = a.act2 + (size_t)kB * I;
+#pragma unroll
+        for (int j = 0; j < MAXQ; j++) {
+            const uint32_t i = j * 256 + tid;
+            t[j] = i < I ? fm_get_tagged(src + i) : ((uint64_t)a.epoch << 32);
+        }
+        uint32_t it = 0;
+        do {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < MAXQ; j++) ready &= (uint32_t)(t[j] >> 32) == a.epoch;
+            if (__all(ready)) break;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < MAXQ; j++) {
+                const uint32_t i = j * 256 + tid;
+                if ((uint32_t)(t[j] >> 32) != a.epoch) t[j] = fm_get_tagged(src + i);
+            }
+        } while (++it < FM_SPIN_MAX);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+#pragma unroll
+        for (int j = 0; j < MAXQ; j++) {
+            const uint32_t i = j * 256 + tid;
+            if (i < I) L.act[i] = __uint_as_float((uint32_t)t[j]);
+        }
+    }
+    __syncthreads();
+    if (doB) {
+        // per-group sums (16 threads x 4 elements per group) and operand rows
+        for (uint32_t g = tid >> 4; g < GI; g += 16) {
+            const float *ag = L.act + 64 * g + 4 * (tid & 15);
+            float s = (ag[0] + ag[1]) + (ag[2] + ag[3]);
+            s = fmm_row_sum(s);
+            if ((tid & 15) == 0) L.asum[g] = s;
+        }
+        const int lay = sB.bits == 4 ? 0 : 1;
+        for (uint32_t e = tid; e < GI * 32; e += 256) fmm_build_pair(L.act + 64 * (e >> 5), sB.bits, e & 31, &L.aq[lay][e >> 5][0]);
+    }
+    __syncthreads();
+    FM_DX_MARK(5);
+    const bool last = (ph & 2) && hasB && a.mode == 0 && kB == a.S - 1;
+    if (doB) {
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        const fm_h2 *aq = &L.aq[sB.bits == 4 ? 0 : 1][0][0];
+        if (sB.bits == 4)
+            fmm_mma<4>(cdn, aq, L.zero, d0, d1);
+        else
+            fmm_mma<2>(cdn, aq, L.zero, d0, d1);
+        float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q]);
+        y = fmm_q_sum(y);
+        const uint32_t row = rowB0 + n;
+        if (lane < 16) {
+            if (a.mode == 1)
+                a.expert_out[(size_t)kB * H + row] = y;
+            else if (!last)
+                fm_put_tagged(&a.y2[(size_t)kB * H + row], y, a.epoch);
+            else
+                L.ylast[16 * wv + n] = y;
+        }
+    } else if (last && lane < 16) {
+        L.ylast[16 * wv + n] = 0.f;
+    }
+
+    FM_DX_MARK(6);
+    // ---- C: the last slot's blocks combine their 64 rows over all slots ----
+    if (last) {
+        __syncthreads();
+        if (wv == 0) {
+            // one wavefront gathers every other slot's y for the 64 rows with
+            // one batch of coherent loads, re-polling only what is not ready
+            const uint32_t row = (b % tilesB) * 64 + lane;
+            uint64_t t[FM_MAX_SLOTS - 1];
+#pragma unroll
+            for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
+                t[k] = (k < a.S - 1 && L.sd[k].valid) ? fm_get_tagged(&a.y2[(size_t)k * H + row])
+                                                     : ((uint64_t)a.epoch << 32);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int k = 0; k < FM_MAX_SLOTS - 1; k++) ready &= (uint32_t)(t[k] >> 32) == a.epoch;
+                if (__all(ready)) break;
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
+                    if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)k * H + row]);
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+            const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+            const float yl = L.ylast[lane];
+            float moe = 0.f;
+#pragma unroll
+            for (int k = 0; k < FM_MAX_SLOTS; k++) {
+                if (k < a.K && L.sd[k].valid) {
+                    const float yk = k == a.S - 1 ? yl : __uint_as_float((uint32_t)t[k < FM_MAX_SLOTS - 1 ? k : 0]);
+                    moe = __fadd_rn(moe, __fmul_rn(L.sd[k].weight, yk));
+                }
+            }
+            float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+            if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, yl));
+            a.out[row] = o;
+            if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+        }
+    }
+    FM_DX_MARK(7);
+}
+
+int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
+    if (a.hidden != FMM_H || a.inter != FMM_MAXI)
+        return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: shape");
+    static int per_cu = -1;
+    if (per_cu < 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_mfma_kernel, 256, 0) != hipSuccess)
+            per_cu = 0;
+    }
+    const uint32_t nA = (uint32_t)a.S * (a.inter / 16), nB = (uint32_t)a.S * (a.hidden / 64);
+    const uint32_t blocks = nA > nB ? nA : nB;
+    // every block may wait on others: the whole grid must be resident
+    if (per_cu < 1 || blocks > (uint32_t)(per_cu * fm_num_cus())) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: grid");
+    hipLaunchKernelGGL(fm_decode_mfma_kernel, dim3(blocks), dim3(256), 0, st, a);
+    return fm_check_launch("fm_decode_mfma_kernel");
+}
