@@ -218,6 +218,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--prefill-warmup", type=int, default=2)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run 10 device copies of MIB MiB (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box has one MI355X); "
@@ -227,6 +229,14 @@ def main():
     import fmoe_amd as fm
     fm.lib()
     dev = torch.device("cuda:0")
+    if args.copy_calib:
+        src = torch.empty(args.copy_calib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 10 x {args.copy_calib} MiB")
+        return
     dec, sample = bench_decode(args, dev)
     log(f"decode: {dec['step_ms'] * 1e3:.2f} us/step, {dec['value']:.0f} GB/s; fused launch "
         f"{dec['roofline']['kernel_us']:.2f} us = {dec['roofline']['achieved']:.0f} GB/s")

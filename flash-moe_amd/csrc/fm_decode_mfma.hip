@@ -27,8 +27,9 @@
 //     The block waits for its slot's I tagged activations, then streams.
 //  C  the blocks of the last slot also combine their 64 rows over all slots
 //     in the slot order of cpu_vec_madd (layer_forward.h:1257, 1295-1305).
-// Every wave issues all of its A and B weight loads before computing, so the
-// whole expert stream is in flight from the first microsecond.
+// Every wave issues all of its gate/up loads before computing, so that stream
+// is in flight from the first microsecond; down-projection loads follow once
+// the wave's own gate/up work is done.
 #include "fm_decode.h"
 
 typedef _Float16 fmm_h8 __attribute__((ext_vector_type(8)));
@@ -243,7 +244,6 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg);
     fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu);
     const uint32_t rowB0 = (b % tilesB) * 64 + 16 * wv;
-    fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn);
 
     FM_DX_MARK(1);
     // ---- x operand rows in both layouts, and the group sums ----
@@ -309,6 +309,10 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     }
 
     FM_DX_MARK(4);
+    // Down-projection loads are issued only now: their data is useless before
+    // the slot's activations exist, and issuing them early would only delay
+    // other waves' gate/up data.
+    fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn);
     // ---- B: stage the slot's activations, then 16 down rows per wave ----
     if (doB) {
         constexpr int MAXQ = FMM_MAXI / 256;
