@@ -41,6 +41,7 @@ typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
 #define FMM_GH (FMM_H / 64)    // input groups of a gate/up row
 #define FMM_GI (FMM_MAXI / 64) // input groups of a down row (max)
 #define FMM_BLOCKS_PER_CU 3
+#define FMM_TS 68  // words per row of a wave's transpose buffer (64 + 4 pad: no bank conflicts)
 #ifndef FM_DX_MARK
 #define FM_DX_MARK(n)
 #endif
@@ -54,6 +55,7 @@ struct __attribute__((aligned(16))) FmmLds {
     float act[FMM_MAXI];      // staged activations (fp32)
     float part[4][16][2];     // per-wave partial gate/up sums of the A rows
     float ylast[64];          // this block's rows of the last slot's y
+    uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
     FmSlot sd[FM_MAX_SLOTS];
 };
 
@@ -111,52 +113,52 @@ FM_DEV float fmm_row_sum(float v) {
     return v;
 }
 
-// Registers of one unit: the codes a lane streams (4 chunks, 32 B per chunk
-// for 4-bit, 16 B for 2-bit) plus its 4-group scale/bias runs.
+// Registers of one unit: 16 rows x 64 words per piece (4-bit: 2 pieces,
+// 2-bit: 1), loaded row-contiguously, plus the lane's scale/bias runs.
 struct FmmCodes {
     fm_u4 c[8];
 };
 
-// Issue the loads of 16 rows x 16 groups (groups g0 .. g0+15 of each row) of
-// one matrix: lane (n = row, kq) loads group g0 + 4c + kq of row n for chunks
-// c = 0..3, and the scale/bias of groups g0 + 4q .. g0 + 4q + 3.
+// Issue the loads of 16 rows x 16 groups (groups g0 .. g0+15) of one matrix.
+// Load j of piece p: lane l reads row row0 + 4j + l/16, words 64p + 4(l%16)
+// .. +3 of the unit -- every instruction covers four 256-byte row runs.  The
+// scale/bias runs follow the MFMA layout: lane (n, kq) takes row row0 + n,
+// groups g0 + 4kq .. g0 + 4kq + 3.
 FM_DEV void fmm_issue(const uint32_t *W, const uint16_t *S, const uint16_t *B, int bits, uint32_t row0,
                       uint32_t in_dim, uint32_t g0, bool ok, FmmCodes &cd, fmm_u2 &sc, fmm_u2 &bi) {
     if (!ok) return;
     const int lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     const uint32_t G = in_dim / 64;
-    const uint32_t row = row0 + n;
     const uint32_t wpg = 2 * bits;  // words per group
-    const uint32_t *wr = W + (size_t)row * (G * wpg);
+    const uint32_t wpr = G * wpg;   // words per row
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        // 4-bit: each load instruction covers 64 contiguous bytes of every row,
-        // half h of chunk c = words 16h + 4kq .. +3 (group 4c + 2h + kq/2);
-        // 2-bit: group 4c + kq (its 4 words)
-        const uint32_t *p = bits == 4 ? wr + (g0 + 4 * c) * 8 + 4 * kq : wr + (g0 + 4 * c + kq) * 4;
-        cd.c[2 * c] = fm_ldg_u4_nt(p);
-        if (bits == 4) cd.c[2 * c + 1] = fm_ldg_u4_nt(p + 16);
+    for (int p = 0; p < 2; p++) {
+        if (p == 1 && bits != 4) break;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t row = row0 + 4 * j + kq;
+            cd.c[4 * p + j] = fm_ldg_u4_nt(W + (size_t)row * wpr + g0 * wpg + 64 * p + 4 * n);
+        }
     }
-    sc = *(const FM_GLOBAL fmm_u2 *)(S + (size_t)row * G + g0 + 4 * kq);
-    bi = *(const FM_GLOBAL fmm_u2 *)(B + (size_t)row * G + g0 + 4 * kq);
+    sc = *(const FM_GLOBAL fmm_u2 *)(S + (size_t)(row0 + n) * G + g0 + 4 * kq);
+    bi = *(const FM_GLOBAL fmm_u2 *)(B + (size_t)(row0 + n) * G + g0 + 4 * kq);
 }
 
-FM_DEV uint32_t fmm_word(const FmmCodes &cd, int c, int wi) {
-    const fm_u4 v = cd.c[2 * c + (wi >> 2)];
-    const int j = wi & 3;
-    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
-}
+FM_DEV uint32_t fmm_comp(const fm_u4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
 
-// 32 MFMAs over 16 groups: D[m][row] += x_op[m] . codes, the x operand row of
-// this lane active only for its (chunk, kq) -- see the file header.  The LDS
-// operand of step j+1 is read during step j; scheduling barriers keep the
-// compiler from hoisting further reads (registers are the scarce resource).
+// 32 MFMAs over 16 groups: D[m][row] += x_op[m] . codes.  Each piece passes
+// through the wave's LDS transpose buffer T: written as loaded (row runs),
+// read back so lane (n, kq) holds row n's words 16h + 4kq .. +3 (h = 0..3).
+// 4-bit: word s of read h of piece p is MFMA (chunk 2p + h/2, i = 4(h%2) + s),
+//        group 4c + 2(i/4) + kq/2 of the unit, word 4(kq%2) + i%4 of it;
+// 2-bit: read h is chunk c = h: group 4c + kq, MFMA i uses word i/2, half i%2.
+// The x operand row m carries group g0 + m and is non-zero only in the slot
+// that holds that group.  The LDS x operand of step j+1 is read during step
+// j; scheduling barriers keep the compiler from hoisting further reads.
 template <int BITS>
-FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, fmm_f4 &d0, fmm_f4 &d1) {
+FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, uint32_t *T, fmm_f4 &d0,
+                    fmm_f4 &d1) {
     const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
-    // Operand row m carries group g0 + m.  4-bit: word i of chunk c in slot kq
-    // belongs to group 4c + 2(i/4) + kq/2 (word 4(kq%2) + i%4 of it); 2-bit:
-    // to group 4c + kq (word i/2, half i%2).
     auto src_of = [&](int j) -> const fm_h2 * {
         const int c = j >> 3, i = j & 7;
         if constexpr (BITS == 4) {
@@ -167,23 +169,34 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
             return on ? xq_grp0 + 32 * m + 4 * i : zero;
         }
     };
+    constexpr int NP = BITS == 4 ? 2 : 1;
     fmm_h8 xo = fmm_lds_op(src_of(0));
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-        const int c = j >> 3, i = j & 7;
-        fmm_h8 xn = xo;
-        if (j + 1 < 32) xn = fmm_lds_op(src_of(j + 1));
-        fmm_h8 co;
-        if constexpr (BITS == 4)
-            co = fmm_codes<4>(fmm_word(cd, c, i), 0);
-        else
-            co = fmm_codes<2>(fmm_word(cd, c, i >> 1), i & 1);
-        if (i & 1)
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d1, 0, 0, 0);
-        else
-            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d0, 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        xo = xn;
+    for (int p = 0; p < NP; p++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(fm_u4 *)&T[(4 * j + kq) * FMM_TS + 4 * m] = cd.c[4 * p + j];
+        fm_u4 v[4];
+#pragma unroll
+        for (int h = 0; h < 4; h++) v[h] = *(const fm_u4 *)&T[m * FMM_TS + 16 * h + 4 * kq];
+        constexpr int NJ = 32 / NP;
+#pragma unroll
+        for (int jj = 0; jj < NJ; jj++) {
+            const int j = p * NJ + jj;
+            const int c = j >> 3, i = j & 7;
+            fmm_h8 xn = xo;
+            if (j + 1 < 32) xn = fmm_lds_op(src_of(j + 1));
+            fmm_h8 co;
+            if constexpr (BITS == 4)
+                co = fmm_codes<4>(fmm_comp(v[2 * (c & 1) + (i >> 2)], i & 3), 0);
+            else
+                co = fmm_codes<2>(fmm_comp(v[c], i >> 1), i & 1);
+            if (i & 1)
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d1, 0, 0, 0);
+            else
+                d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d0, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            xo = xn;
+        }
     }
 }
 
@@ -284,11 +297,11 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[sA.bits == 4 ? 0 : 1][16 * wv][0];
         if (sA.bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, g0, g1);
-            fmm_mma<4>(cu, xq, L.zero, u0, u1);
+            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1);
+            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1);
         } else {
-            fmm_mma<2>(cg, xq, L.zero, g0, g1);
-            fmm_mma<2>(cu, xq, L.zero, u0, u1);
+            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1);
+            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1);
         }
         const float *gs4 = &L.xsum[16 * wv + 4 * q];
         float pg = fmm_fold(g0 + g1, sg, bg, gs4);
@@ -362,9 +375,9 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &L.aq[sB.bits == 4 ? 0 : 1][0][0];
         if (sB.bits == 4)
-            fmm_mma<4>(cdn, aq, L.zero, d0, d1);
+            fmm_mma<4>(cdn, aq, L.zero, L.tr[wv], d0, d1);
         else
-            fmm_mma<2>(cdn, aq, L.zero, d0, d1);
+            fmm_mma<2>(cdn, aq, L.zero, L.tr[wv], d0, d1);
         float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q]);
         y = fmm_q_sum(y);
         const uint32_t row = rowB0 + n;
