@@ -44,6 +44,18 @@ def make_pool(bits_of, seed):
     return pool, sample, np
 
 
+def pmc_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE in KiB per dispatch, each scaled by what the counter reads for a plain
+    device copy of known size); None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return round(d["fetch_kib"] * 1024 * d["fetch_scale"] + d["write_kib"] * 1024 * d["write_scale"])
+
+
 def bench_decode(args, dev):
     import numpy as np
     import torch
@@ -88,16 +100,17 @@ def bench_decode(args, dev):
     # algorithmic bytes per step: K routed + shared blobs, x, h_mid, out fp32 + bf16
     blob = fm.layout_of(H, I, 64, 4).size
     step_bytes = (K + 1) * blob + H * 4 * 3 + H * 2 + E * 4
-    # fused expert launch pair alone, timed per call with events on its stream
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for j, i in enumerate(range(args.warmup, nsteps)):
-        fm.route_topk(logits[i:i + 1], K, idx[i], w[i])
-        evs[j][0].record()
+    # the fused expert kernel alone: back-to-back launches (routing already
+    # done above for every step) between two events on its stream
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record()
+    for i in range(args.warmup, nsteps):
         fm.moe_decode_pool(pool, idx[i], w[i], x, out, ws, shared=shared[i % n_sh], shared_bits=4,
                            shared_score=scores[i:i + 1], h_mid=hm, out_bf16=ob)
-        evs[j][1].record()
+    k1.record()
     torch.cuda.synchronize()
-    kern_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    kern_ms = k0.elapsed_time(k1) / args.steps
     kern_bytes = (K + 1) * blob + H * 4 * 3 + H * 2
     # unique experts actually touched per step (routing may repeat across steps, never within)
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
@@ -105,8 +118,8 @@ def bench_decode(args, dev):
         "step_ms": step_ms, "wall_s": wall, "step_bytes": step_bytes,
         "value": step_bytes / (step_ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "fm_decode_gateup_kernel + fm_decode_down_kernel (one fm_moe_decode_pool call)",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": pmc_traffic("decode_config2_pmc.json"),
+                     "kernel": "fm_decode_mfma_kernel (one fm_moe_decode_pool call)",
                      "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes},
     }
     return res, sample_blobs
