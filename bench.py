@@ -174,6 +174,72 @@ def bench_prefill(args, dev, pool):
             "bytes_per_step": bytes_step, "flops_per_step": flops}
 
 
+def bench_tiered(args, dev):
+    """Config 4: the config-2 layer with 128 hot 4-bit experts (seeded
+    permutation) and 384 cold 2-bit ones; decode at batch 1 (route + fused
+    step) and batch 4 (route 4 tokens + grouped expert kernel over the union of
+    their experts).  Bytes = unique selected blobs + shared + activations."""
+    import numpy as np
+    import torch
+    import fmoe_amd as fm
+    from fmoe_amd import synth
+    perm = synth.rng_for(3201).permutation(E)
+    hot = set(int(e) for e in perm[:128])
+    bits_of = lambda e: 4 if e in hot else 2  # noqa: E731
+    pool, _, _ = make_pool(bits_of, 3200)
+    rng = synth.rng_for(3202)
+    sizes = {b: fm.layout_of(H, I, 64, b).size for b in (2, 4)}
+    sh_blob = torch.from_numpy(synth.expert_blob((3203, 0), H, I, 4)).to(dev)
+    sh = fm.experts_from_blob(sh_blob, 4, H, I)
+    res = {}
+    for B in (1, 4):
+        n = args.warmup + args.steps
+        logits = torch.from_numpy(rng.normal(0, 1, (n, B, E)).astype(np.float32)).to(dev)
+        scores = torch.from_numpy(rng.normal(0, 1, (n, B)).astype(np.float32)).to(dev)
+        X = torch.from_numpy(synth.hidden_vec(rng, H, (B, H))).to(dev)
+        hm = torch.from_numpy(rng.normal(0, 1, (B, H)).astype(np.float32)).to(dev)
+        idx = torch.empty((n, B, K), dtype=torch.int32, device=dev)
+        w = torch.empty((n, B, K), dtype=torch.float32, device=dev)
+        out = torch.empty((B, H), dtype=torch.float32, device=dev)
+        ob = torch.empty((B, H), dtype=torch.int16, device=dev)
+        if B == 1:
+            ws = torch.zeros(fm.decode_workspace_bytes(K + 1, H, I), dtype=torch.uint8, device=dev)
+        else:
+            ws = torch.empty(fm.prefill_workspace_bytes(B, K, pool), dtype=torch.uint8, device=dev)
+
+        def step(i):
+            fm.route_topk(logits[i], K, idx[i], w[i])
+            if B == 1:
+                fm.moe_decode_pool(pool, idx[i, 0], w[i, 0], X[0], out[0], ws, shared=sh, shared_bits=4,
+                                   shared_score=scores[i, :1], h_mid=hm[0], out_bf16=ob[0])
+            else:
+                fm.prefill_moe(pool, idx[i], w[i], X, out, ws, shared=sh, shared_bits=4, shared_scores=scores[i],
+                               h_mid=hm, out_bf16=ob)
+
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.warmup, n):
+            step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        ids = idx[args.warmup:].cpu().numpy()
+        nbytes = []
+        for i in range(args.steps):
+            u = np.unique(ids[i])
+            nbytes.append(sum(sizes[bits_of(int(e))] for e in u) + sizes[4] + B * H * (4 * 3 + 2))
+        step_bytes = float(np.mean(nbytes))
+        res[f"b{B}"] = {"us_per_step": ms * 1e3, "bytes_per_step": round(step_bytes),
+                        "gbs": step_bytes / (ms * 1e-3) / 1e9,
+                        "hbm_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                        "path": "route + fm_moe_decode_pool" if B == 1 else "route + fm_prefill_moe (grouped)"}
+    del pool
+    return res
+
+
 def cpu_baseline(sample_blobs, budget_s=10.0):
     """The reference's own CPU kernels (oracle/_ref: cpu_dequant_matvec +
     cpu_swiglu + cpu_vec_madd, one core) on config-2 steps until ~budget_s."""
@@ -231,6 +297,7 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--prefill-warmup", type=int, default=2)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-tiered", action="store_true")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 10 device copies of MIB MiB (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -257,6 +324,10 @@ def main():
     if pre:
         log(f"prefill: {pre['ms']:.3f} ms/layer, {pre['tokens_per_s']:.0f} tok/s, {pre['hbm_gbs']:.0f} GB/s, "
             f"{pre['tflops']:.1f} TFLOP/s")
+    tiered = None if args.no_tiered else bench_tiered(args, dev)
+    if tiered:
+        for k, v in tiered.items():
+            log(f"tiered {k}: {v['us_per_step']:.2f} us/step, {v['gbs']:.0f} GB/s ({v['path']})")
     cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_budget)
     line = {
         "metric": "4-bit expert FFN decode GB/s (% of HBM peak); prefill MoE-layer tokens/s",
@@ -273,6 +344,10 @@ def main():
             "tokens_per_s": round(pre["tokens_per_s"]), "ms_per_layer": pre["ms"],
             "unique_experts": pre["unique_experts"], "hbm_gbs": round(pre["hbm_gbs"], 1),
             "hbm_frac": pre["hbm_frac"], "tflops": round(pre["tflops"], 2), "mfma_frac": pre["mfma_frac"]},
+        "tiered": None if tiered is None else {
+            "workload": "config 4: config-2 layer with 128 hot 4-bit + 384 cold 2-bit experts, "
+                        "top-10 + 4-bit shared, batch 1 and 4", **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                                                  for kk, vv in v.items()} for k, v in tiered.items()}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
