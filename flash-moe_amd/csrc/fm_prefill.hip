@@ -34,6 +34,7 @@ typedef float fm_f4v __attribute__((ext_vector_type(4)));
 #define PF_TOK 16          // token columns per chunk (one MFMA N tile)
 #define PF_FEAT_WAVE 64    // output features per wave (4 MFMA M tiles)
 #define PF_KB 8            // groups per LDS stage (512 inputs)
+#define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: one fused decode step per token
 
 // One expert's matrices.
 struct PfMat {
@@ -514,6 +515,26 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     PfLayout L = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, has_shared);
     if (!ws || ws_bytes < L.total)
         return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", who, ws_bytes, L.total);
+    // A few tokens (batched decode): one fused decode step per token streams
+    // each token's experts once at decode efficiency; the grouped GEMM only pays
+    // off once experts are shared by many tokens.  Same result per token
+    // (batched_prefill.h:241-308 is per-token decode arithmetic).
+    if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K) {
+        const size_t dws = fm_moe_decode_workspace_size(K + has_shared, pool->hidden, pool->inter);
+        if (dws <= ws_bytes) {
+            for (int t = 0; t < T; t++) {
+                const int rc = fm_moe_decode_pool(pool, K, idx + (size_t)t * K, weights + (size_t)t * K, shared,
+                                                  shared_bits, shared_gate_scores ? shared_gate_scores + t : nullptr,
+                                                  X + (size_t)t * pool->hidden,
+                                                  h_mid ? h_mid + (size_t)t * pool->hidden : nullptr,
+                                                  out + (size_t)t * pool->hidden,
+                                                  out_bf16 ? out_bf16 + (size_t)t * pool->hidden : nullptr, ws, dws,
+                                                  stream);
+                if (rc) return rc;
+            }
+            return FM_OK;
+        }
+    }
     char *p = (char *)ws;
     hipStream_t st = fm_stream(stream);
     const uint32_t mc = pf_max_chunks(T, K, pool->num_experts, has_shared);
