@@ -111,6 +111,17 @@ def bench_decode(args, dev):
     k1.record()
     torch.cuda.synchronize()
     kern_ms = k0.elapsed_time(k1) / args.steps
+    # the same launches with the next layer's input RMS norm fused into the combine
+    nw = torch.from_numpy(synth.bf16_bits(rng.normal(1, 0.1, H).astype(np.float32)).view(np.int16)).to(dev)
+    normed = torch.empty(H, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    k0.record()
+    for i in range(args.warmup, nsteps):
+        fm.moe_decode_pool_norm(pool, idx[i], w[i], x, out, ws, nw, 1e-6, normed, shared=shared[i % n_sh],
+                                shared_bits=4, shared_score=scores[i:i + 1], h_mid=hm, out_bf16=ob)
+    k1.record()
+    torch.cuda.synchronize()
+    norm_ms = k0.elapsed_time(k1) / args.steps
     kern_bytes = (K + 1) * blob + H * 4 * 3 + H * 2
     # unique experts actually touched per step (routing may repeat across steps, never within)
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
@@ -120,7 +131,8 @@ def bench_decode(args, dev):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": pmc_traffic("decode_config2_pmc.json"),
                      "kernel": "fm_decode_mfma_kernel (one fm_moe_decode_pool call)",
-                     "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes},
+                     "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes,
+                     "kernel_us_with_fused_rms_norm": norm_ms * 1e3},
     }
     return res, sample_blobs
 

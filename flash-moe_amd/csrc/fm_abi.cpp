@@ -38,6 +38,9 @@ int fm_check_dims(const char *who, uint32_t out_dim, uint32_t in_dim, uint32_t g
 
 extern "C" const char *fm_last_error(void) { return g_err; }
 
+// Error reporting for the host C layer driver (same thread-local message).
+extern "C" int fm_host_fail(int code, const char *msg) { return fm_fail(code, "%s", msg); }
+
 extern "C" const char *fm_version(void) { return "flash-moe-amd 0.1 (gfx950)"; }
 
 // config.h:94-137: nine tensors in the order gate_w, gate_s, gate_b, up_w,

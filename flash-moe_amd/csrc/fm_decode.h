@@ -42,6 +42,11 @@ struct FmDecodeArgs {
     uint32_t *err;   // set when a bounded wait gave up
     uint32_t epoch;  // this call's tag (never 0)
     int phases;      // mfma kernel: bit 0 gate/up, bit 1 down+combine (0 = both)
+    // optional next-layer input RMS norm of out (cpu_kernels.h:235-246)
+    const uint16_t *norm_w;  // bf16 [hidden] or NULL
+    float norm_eps;
+    float *normed;           // fp32 [hidden]
+    uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
 };
 
 __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
@@ -91,3 +96,7 @@ __device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
 // each returns FM_ERR_UNSUPPORTED (message cleared by the caller) when the
 // shape or slot mix is outside what it implements.
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st);
+
+// Standalone RMS norm launch (fm_rms_norm's kernel) for paths without the fused one.
+int fm_launch_rms_norm(const float *x, const uint16_t *w, uint32_t dim, float eps, float *out, uint16_t *out_bf16,
+                       hipStream_t st);

@@ -678,10 +678,12 @@ static int fm_check_expert(const char *who, int k, const fm_expert_weights &e, i
 }
 
 // Workspace: [err word, 256 B] [act2: S x inter x 8 B] [y2: S x hidden x 8 B]
+// [ss2: hidden/64 x 8 B tagged partial sums of squares for the fused RMS norm]
 // Tags make stale contents harmless, so the workspace needs no initialisation.
 extern "C" size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter) {
     if (n_slots < 1) n_slots = 1;
-    return 256 + fm_align_up((size_t)n_slots * inter * 8, 256) + fm_align_up((size_t)n_slots * hidden * 8, 256);
+    return 256 + fm_align_up((size_t)n_slots * inter * 8, 256) + fm_align_up((size_t)n_slots * hidden * 8, 256) +
+           fm_align_up((size_t)(hidden + 63) / 64 * 8, 256);
 }
 
 static uint32_t fm_next_epoch() {
@@ -753,7 +755,21 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     a.act2 = (uint64_t *)p;
     p += fm_align_up((size_t)a.S * a.inter * 8, 256);
     a.y2 = (uint64_t *)p;
+    p += fm_align_up((size_t)a.S * a.hidden * 8, 256);
+    a.ss2 = (uint64_t *)p;
     a.epoch = fm_next_epoch();
+    if (a.norm_w) {
+        // the fused kernel normalises in its combine; every other path runs
+        // the standalone norm after the step
+        int rc = fm_launch_decode_mfma(a, st);
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
+        FmDecodeArgs b = a;
+        b.norm_w = nullptr;
+        rc = fm_decode_launch(b, ws, ws_bytes, st);
+        if (rc) return rc;
+        return fm_launch_rms_norm(a.out, a.norm_w, a.hidden, a.norm_eps, a.normed, nullptr, st);
+    }
     if (((size_t)a.hidden + 4 * (size_t)a.inter) * sizeof(float) > 65536)
         return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden + 4*inter must be <= 16384 floats", who);
     int lh, gh, li, gi;
@@ -820,13 +836,11 @@ extern "C" int fm_moe_decode(int K, const fm_expert_weights *experts, const int 
     return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
 }
 
-extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
-                                  const float *weights, const fm_expert_weights *shared,
-                                  int shared_bits, const float *shared_gate_score,
-                                  const float *x, const float *h_mid, float *out,
-                                  uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
-    const char *who = "fm_moe_decode_pool";
-    fm_clear_error();
+static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int K, const int *idx,
+                               const float *weights, const fm_expert_weights *shared, int shared_bits,
+                               const float *shared_gate_score, const float *x, const float *h_mid, float *out,
+                               uint16_t *out_bf16, const uint16_t *norm_w, float norm_eps, float *normed, void *ws,
+                               size_t ws_bytes, void *stream) {
     FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
     FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
     FM_REQUIRE(K == 0 || (idx && weights), "%s: NULL idx/weights", who);
@@ -841,6 +855,9 @@ extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *
         a.off4[i] = l4.off[i];
         a.off2[i] = l2.off[i];
     }
+    a.norm_w = norm_w;
+    a.norm_eps = norm_eps;
+    a.normed = normed;
     a.pool_mode = 1;
     a.pool_blobs = pool->blobs;
     a.pool_bits = pool->bits;
@@ -865,6 +882,27 @@ extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *
     a.out = out;
     a.out_bf16 = out_bf16;
     return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
+}
+
+extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
+                                  const fm_expert_weights *shared, int shared_bits, const float *shared_gate_score,
+                                  const float *x, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
+                                  size_t ws_bytes, void *stream) {
+    fm_clear_error();
+    return fm_decode_pool_impl("fm_moe_decode_pool", pool, K, idx, weights, shared, shared_bits, shared_gate_score, x,
+                               h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream);
+}
+
+extern "C" int fm_moe_decode_pool_norm(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
+                                       const fm_expert_weights *shared, int shared_bits,
+                                       const float *shared_gate_score, const float *x, const float *h_mid,
+                                       float *out, uint16_t *out_bf16, const uint16_t *norm_w, float eps,
+                                       float *normed, void *ws, size_t ws_bytes, void *stream) {
+    fm_clear_error();
+    FM_REQUIRE(norm_w && normed, "fm_moe_decode_pool_norm: NULL norm weights or output");
+    FM_REQUIRE(eps >= 0.f, "fm_moe_decode_pool_norm: eps < 0");
+    return fm_decode_pool_impl("fm_moe_decode_pool_norm", pool, K, idx, weights, shared, shared_bits,
+                               shared_gate_score, x, h_mid, out, out_bf16, norm_w, eps, normed, ws, ws_bytes, stream);
 }
 
 extern "C" int fm_encode_experts_batched(int K, const int *valid, const fm_expert_weights *experts,

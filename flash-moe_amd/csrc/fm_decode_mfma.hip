@@ -432,12 +432,32 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
             if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, yl));
             a.out[row] = o;
             if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+            if (a.norm_w) {
+                // next layer's input RMS norm (cpu_kernels.h:235-246): every
+                // combining block publishes the sum of squares of its 64 rows,
+                // then reduces all of them in the same fixed order
+                const uint32_t j = b % tilesB;
+                const float sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(o * o))));
+                if (lane == 0) fm_put_tagged(&a.ss2[j], sq, a.epoch);
+                uint64_t v = lane < (int)tilesB ? fm_get_tagged(&a.ss2[lane]) : ((uint64_t)a.epoch << 32);
+                uint32_t it = 0;
+                while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.ss2[lane]);
+                }
+                if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+                const float part = lane < (int)tilesB ? __uint_as_float((uint32_t)v) : 0.f;
+                const float tot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(part))));
+                const float inv = 1.0f / sqrtf(tot / (float)H + a.norm_eps);
+                a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
+            }
         }
     }
     FM_DX_MARK(7);
 }
 
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
+    if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
     if (a.hidden != FMM_H || a.inter != FMM_MAXI)
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: shape");
     static int per_cu = -1;

@@ -79,6 +79,9 @@ SIGNATURES = {
                             I32, F32, U32, U32, U32, P, P, P, P, P, SZ, P]),
     "fm_moe_decode_pool": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
                                  I32, P, P, P, P, P, P, SZ, P]),
+    "fm_moe_decode_pool_norm": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
+                                      I32, P, P, P, P, P, P, F32, P, P, SZ, P]),
+    "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),
     "fm_route_topk": (I32, [P, I32, I32, I32, P, P, P]),
     "fm_prefill_moe_workspace_size": (SZ, [I32, I32, ctypes.POINTER(ExpertPool)]),
     "fm_prefill_moe": (I32, [ctypes.POINTER(ExpertPool), I32, I32, P, P, ctypes.POINTER(ExpertWeights),
@@ -87,6 +90,7 @@ SIGNATURES = {
     "fm_pfb_gemm": (I32, [P, P, P, P, P, U32, U32, U32, U32, I32, P, SZ, P]),
     "fm_moe_forward_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32]),
     "fm_moe_forward": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, SZ, P]),
+    "fm_moe_forward_norm": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_moe_prefill_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32, I32]),
     "fm_moe_prefill_forward": (I32, [ctypes.POINTER(MoeLayer), I32, I32, P, P, P, P, P, SZ, P]),
 }

@@ -15,6 +15,7 @@ __all__ = [
     "moe_decode", "moe_decode_pool", "encode_experts_batched", "moe_combine", "route_topk",
     "prefill_workspace_bytes", "prefill_moe", "pfb_gemm", "DevicePool", "moe_forward",
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
+    "moe_decode_pool_norm", "rms_norm", "moe_forward_norm",
 ]
 
 
@@ -85,6 +86,19 @@ def moe_decode_pool(pool, idx, weights, x, out, ws, shared=None, shared_bits=4, 
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
         shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
         ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def moe_decode_pool_norm(pool, idx, weights, x, out, ws, norm_w, eps, normed, shared=None, shared_bits=4,
+                         shared_score=None, h_mid=None, out_bf16=None, stream=None):
+    K = idx.numel()
+    check(lib().fm_moe_decode_pool_norm(
+        ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
+        shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(norm_w), float(eps),
+        ptr(normed), ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def rms_norm(x, w_bf16, eps, out, out_bf16=None, stream=None):
+    check(lib().fm_rms_norm(ptr(x), ptr(w_bf16), x.numel(), float(eps), ptr(out), ptr(out_bf16), stream_ptr(stream)))
 
 
 def encode_experts_batched(experts, bits, x, expert_out, ws, hidden, inter, valid=None, stream=None):
@@ -164,6 +178,12 @@ def moe_forward_workspace_bytes(layer, K):
 def moe_forward(layer, K, h_post, h_mid, out, ws, out_bf16=None, stream=None):
     check(lib().fm_moe_forward(ctypes.byref(layer), K, ptr(h_post), ptr(h_mid), ptr(out), ptr(out_bf16),
                                ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def moe_forward_norm(layer, K, h_post, h_mid, out, ws, norm_w, eps, normed, out_bf16=None, stream=None):
+    check(lib().fm_moe_forward_norm(ctypes.byref(layer), K, ptr(h_post), ptr(h_mid), ptr(out), ptr(out_bf16),
+                                    ptr(norm_w), float(eps), ptr(normed), ptr(ws), ws.numel() * ws.element_size(),
+                                    stream_ptr(stream)))
 
 
 def moe_prefill_workspace_bytes(layer, K, T):

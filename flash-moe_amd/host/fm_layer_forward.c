@@ -13,6 +13,9 @@
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+/* sets fm_last_error() (fm_abi.cpp) and returns code */
+int fm_host_fail(int code, const char *msg);
+
 static int layer_ok(const fm_moe_layer *L, int K) {
     return L && L->router_w && L->router_s && L->router_b && L->pool.num_experts > 0 && K >= 1 &&
            K <= FM_MAX_K && (!L->has_shared || (L->seg_w && L->seg_s && L->seg_b));
@@ -28,11 +31,14 @@ size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K) {
     return n;
 }
 
-int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
-                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
-    if (!layer_ok(L, K) || !h_post || !out) return FM_ERR_INVALID;
+static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                            float *out, uint16_t *out_bf16, const uint16_t *norm_w, float eps, float *normed,
+                            void *ws, size_t ws_bytes, void *stream) {
+    (void)who;
+    if (!layer_ok(L, K)) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward: incomplete layer or K outside 1..FM_MAX_K");
+    if (!h_post || !out) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward: NULL h_post or out");
     size_t need = fm_moe_forward_workspace_size(L, K);
-    if (!ws || ws_bytes < need) return FM_ERR_WORKSPACE;
+    if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_forward: workspace too small");
     char *p = (char *)ws;
     float *logits = (float *)p;
     p += align256((size_t)L->pool.num_experts * sizeof(float));
@@ -55,10 +61,29 @@ int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const floa
     /* softmax -> top-K -> renormalise (3519-3523) */
     rc = fm_route_topk(logits, 1, (int)L->pool.num_experts, K, idx, w, stream);
     if (rc) return rc;
-    /* CMD3: experts + shared expert + combine (3895-3993) */
+    /* CMD3: experts + shared expert + combine (3895-3993), optionally the next
+     * layer's input RMS norm (3995-4029) */
+    if (norm_w)
+        return fm_moe_decode_pool_norm(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL, L->shared_bits,
+                                       L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16, norm_w, eps,
+                                       normed, p, rest, stream);
     return fm_moe_decode_pool(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL,
                               L->shared_bits, L->has_shared ? seg : NULL, h_post, h_mid, out,
                               out_bf16, p, rest, stream);
+}
+
+int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
+    return moe_forward_impl("fm_moe_forward", L, K, h_post, h_mid, out, out_bf16, NULL, 0.f, NULL, ws, ws_bytes,
+                            stream);
+}
+
+int fm_moe_forward_norm(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid, float *out,
+                        uint16_t *out_bf16, const uint16_t *next_norm_w, float eps, float *normed, void *ws,
+                        size_t ws_bytes, void *stream) {
+    if (!next_norm_w || !normed) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward_norm: NULL norm weights or output");
+    return moe_forward_impl("fm_moe_forward_norm", L, K, h_post, h_mid, out, out_bf16, next_norm_w, eps, normed, ws,
+                            ws_bytes, stream);
 }
 
 size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
@@ -75,9 +100,10 @@ size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
 int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
                            const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
                            size_t ws_bytes, void *stream) {
-    if (!layer_ok(L, K) || T <= 0 || !h_post || !out) return FM_ERR_INVALID;
+    if (!layer_ok(L, K)) return fm_host_fail(FM_ERR_INVALID, "fm_moe_prefill_forward: incomplete layer or bad K");
+    if (T <= 0 || !h_post || !out) return fm_host_fail(FM_ERR_INVALID, "fm_moe_prefill_forward: T <= 0 or NULL buffer");
     size_t need = fm_moe_prefill_workspace_size(L, K, T);
-    if (!ws || ws_bytes < need) return FM_ERR_WORKSPACE;
+    if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_prefill_forward: workspace too small");
     char *p = (char *)ws;
     float *logits = (float *)p;
     p += align256((size_t)T * L->pool.num_experts * sizeof(float));

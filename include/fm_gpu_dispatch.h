@@ -119,12 +119,12 @@ int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *
 /* Decode: K routed experts + shared expert, SwiGLU, weighted combine        */
 /* ------------------------------------------------------------------------ */
 
-/* Workspace bytes for fm_moe_decode / fm_moe_decode_pool /
+/* Workspace bytes for fm_moe_decode / fm_moe_decode_pool(_norm) /
  * fm_encode_experts_batched with n_slots = K (+1 if a shared expert).
- * The workspace holds a small control block of counters: it must be
- * zero-filled (e.g. hipMemset) before its first use and 256-byte aligned;
- * every call leaves the counters at zero again.  Calls that share one
- * workspace must be ordered (same stream); concurrent calls need their own. */
+ * The workspace must be 256-byte aligned and needs no initialisation: values
+ * handed between waves carry a per-call tag, so stale contents are ignored.
+ * Calls that share one workspace must be ordered (same stream); concurrent
+ * calls need their own. */
 size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
 
 /* K expert FFNs sharing input x, one output per expert:
@@ -172,6 +172,25 @@ int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
                        int shared_bits, const float *shared_gate_score,
                        const float *x, const float *h_mid, float *out,
                        uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
+
+/* fm_moe_decode_pool plus the next layer's input RMS norm of `out` (CMD3 Enc
+ * C2/C3, layer_forward.h:3995-4029; rms_norm_sum_sq / rms_norm_apply_bf16,
+ * shaders.metal:792-870; CPU semantics cpu_rms_norm, cpu_kernels.h:235-246):
+ *   normed[i] = out[i] / sqrt(mean(out^2) + eps) * norm_w[i]
+ * norm_w: device bf16 [hidden]; normed: device fp32 [hidden].  Fused into the
+ * combine where the fused kernel runs, otherwise one extra launch. */
+int fm_moe_decode_pool_norm(const fm_expert_pool *pool, int K, const int *idx,
+                            const float *weights, const fm_expert_weights *shared,
+                            int shared_bits, const float *shared_gate_score,
+                            const float *x, const float *h_mid, float *out,
+                            uint16_t *out_bf16, const uint16_t *norm_w, float eps,
+                            float *normed, void *ws, size_t ws_bytes, void *stream);
+
+/* RMS norm with bf16 weights (cpu_rms_norm, cpu_kernels.h:235-246):
+ *   out[i] = x[i] / sqrt(sum(x^2) / dim + eps) * w[i]
+ * x, out: device fp32 [dim]; w: device bf16 [dim]; out_bf16 optional (RNE). */
+int fm_rms_norm(const float *x, const uint16_t *w, uint32_t dim, float eps, float *out,
+                uint16_t *out_bf16, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Routing                                                                   */

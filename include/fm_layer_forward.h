@@ -38,6 +38,15 @@ size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K);
 int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
                    float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
 
+/* fm_moe_forward plus the next layer's input RMS norm of `out`, as CMD3 Enc
+ * C2/C3 do (layer_forward.h:3995-4029, cpu_rms_norm cpu_kernels.h:235-246):
+ *   normed[i] = out[i] / sqrt(mean(out^2) + eps) * next_norm_w[i]
+ * next_norm_w: device bf16 [hidden]; normed: device fp32 [hidden].  Same
+ * workspace as fm_moe_forward. */
+int fm_moe_forward_norm(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid, float *out,
+                        uint16_t *out_bf16, const uint16_t *next_norm_w, float eps, float *normed, void *ws,
+                        size_t ws_bytes, void *stream);
+
 size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T);
 
 /* Prefill of T tokens: the MoE part of batched_prefill (batched_prefill.h:

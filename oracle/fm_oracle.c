@@ -147,6 +147,15 @@ void fmo_swiglu(const float *gate, const float *up, float *out, int dim) {
 float fmo_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 /* cpu_kernels.h:263-277: max, exp(x-max) with a sequential sum, times 1/sum */
+/* cpu_kernels.h:235-246 */
+void fmo_rms_norm(const float *x, const uint16_t *w_bf16, float *out, int dim, float eps) {
+    float sum_sq = 0.0f;
+    for (int i = 0; i < dim; i++) sum_sq += x[i] * x[i];
+    const float rms = sqrtf(sum_sq / dim + eps);
+    const float inv_rms = 1.0f / rms;
+    for (int i = 0; i < dim; i++) out[i] = x[i] * inv_rms * fmo_bf16_to_f32(w_bf16[i]);
+}
+
 void fmo_softmax(float *x, int dim) {
     float mx = x[0];
     for (int i = 1; i < dim; i++)

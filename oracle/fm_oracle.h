@@ -48,7 +48,10 @@ void fmo_pack_codes(int bits, const uint8_t *codes, size_t n_codes, uint32_t *pa
 
 void fmo_swiglu(const float *gate, const float *up, float *out, int dim);   /* cpu_kernels.h:249-255 */
 float fmo_sigmoid(float x);                                                /* cpu_kernels.h:258-260 */
-void fmo_softmax(float *x, int dim);                                       /* cpu_kernels.h:263-277 */
+void fmo_softmax(float *x, int dim);
+/* cpu_kernels.h:235-246 -- RMS norm with bf16 weights: sequential sum of
+ * squares, rms = sqrtf(sum/dim + eps), out = x * (1/rms) * w */
+void fmo_rms_norm(const float *x, const uint16_t *w_bf16, float *out, int dim, float eps);                                       /* cpu_kernels.h:263-277 */
 void fmo_topk(const float *scores, int dim, int K, int *indices, float *values); /* cpu_kernels.h:280-299 */
 void fmo_normalize_weights(float *w, int K);                               /* cpu_kernels.h:302-309 */
 void fmo_vec_madd(float *dst, const float *src, float scale, int dim);     /* cpu_kernels.h:318-321 */

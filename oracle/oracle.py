@@ -45,6 +45,7 @@ class OracleLib:
             "fmo_swiglu": (None, [_P, _P, _P, _I]),
             "fmo_sigmoid": (_F, [_F]),
             "fmo_softmax": (None, [_P, _I]),
+            "fmo_rms_norm": (None, [_P, _P, _P, _I, _F]),
             "fmo_topk": (None, [_P, _I, _I, _P, _P]),
             "fmo_normalize_weights": (None, [_P, _I]),
             "fmo_vec_madd": (None, [_P, _P, _F, _I]),
@@ -102,6 +103,12 @@ class OracleLib:
         x = _c(x, np.float32).copy()
         self.L.fmo_softmax(_p(x), x.size)
         return x
+
+    def rms_norm(self, x, w_bf16, eps):
+        x, w = _c(x, np.float32), _c(w_bf16, np.uint16)
+        o = np.empty_like(x)
+        self.L.fmo_rms_norm(_p(x), _p(w), _p(o), x.size, eps)
+        return o
 
     def topk(self, scores, K):
         scores = _c(scores, np.float32)
@@ -193,6 +200,7 @@ class RefLib:
             "ref_cpu_topk": (None, [_P, _I, _I, _P, _P]),
             "ref_cpu_normalize_weights": (None, [_P, _I]),
             "ref_cpu_vec_madd": (None, [_P, _P, _F, _I]),
+            "ref_cpu_rms_norm": (None, [_P, _P, _P, _I, _F]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -218,6 +226,12 @@ class RefLib:
         x = _c(x, np.float32).copy()
         self.L.ref_cpu_softmax(_p(x), x.size)
         return x
+
+    def rms_norm(self, x, w_bf16, eps):
+        x, w = _c(x, np.float32), _c(w_bf16, np.uint16)
+        o = np.empty_like(x)
+        self.L.ref_cpu_rms_norm(_p(x), _p(w), _p(o), x.size, eps)
+        return o
 
     def topk(self, scores, K):
         scores = _c(scores, np.float32)

@@ -18,3 +18,4 @@ void ref_cpu_softmax(float *x, int dim) { cpu_softmax(x, dim); }
 void ref_cpu_topk(const float *s, int dim, int K, int *idx, float *val) { cpu_topk(s, dim, K, idx, val); }
 void ref_cpu_normalize_weights(float *w, int K) { cpu_normalize_weights(w, K); }
 void ref_cpu_vec_madd(float *d, const float *s, float sc, int dim) { cpu_vec_madd(d, s, sc, dim); }
+void ref_cpu_rms_norm(const float *x, const uint16_t *w, float *o, int dim, float eps) { cpu_rms_norm(x, w, o, dim, eps); }

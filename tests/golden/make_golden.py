@@ -60,6 +60,10 @@ def main():
     out.update(bf_in=bits, bf_f32=np.array([ref.L.ref_bf16_to_f32(int(v)) for v in bits], np.float32))
     f = rng.normal(0, 10, 64).astype(np.float32)
     out.update(tr_in=f, tr_out=np.array([ref.L.ref_f32_to_bf16(float(v)) for v in f], np.uint16))
+    # RMS norm with bf16 weights (cpu_kernels.h:235-246)
+    x = rng.normal(0, 2, 4096).astype(np.float32)
+    wn = synth.bf16_bits(rng.normal(1, 0.2, 4096).astype(np.float32))
+    out.update(rn_x=x, rn_w=wn, rn_eps=np.float32(1e-6), rn_y=ref.rms_norm(x, wn, np.float32(1e-6)))
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_kernels.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, os.path.getsize(path), "bytes")

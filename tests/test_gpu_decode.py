@@ -230,3 +230,59 @@ def test_moe_forward_layer(orc, dev, pool64):
     ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], hp, HIDDEN, INTER,
                          shared_blob=shared_blob, shared_bits=4, shared_score=float(score), h_mid=hm)
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+@pytest.mark.parametrize("dim", [4096, 777, 1, 16384])
+def test_rms_norm_vs_oracle(orc, dev, dim):
+    """fm_rms_norm vs cpu_rms_norm (cpu_kernels.h:235-246); the device sums squares
+    as a tree, so results agree to fp32 rounding (bar 1e-5), bf16 outputs to 2e-2."""
+    import torch
+    say("rms_norm", dim)
+    rng = synth.rng_for(21, dim)
+    x = rng.normal(0, 2, dim).astype(np.float32)
+    w = synth.bf16_bits(rng.normal(1, 0.2, dim).astype(np.float32))
+    out = torch.empty(dim, dtype=torch.float32, device=dev)
+    ob = torch.empty(dim, dtype=torch.int16, device=dev)
+    fm.rms_norm(T(x, dev), T(w.view(np.int16), dev), 1e-6, out, ob)
+    torch.cuda.synchronize()
+    ref = orc.rms_norm(x, w, 1e-6)
+    assert norm_err(out.cpu().numpy(), ref) <= 1e-5
+    assert norm_err(bf16_out(ob.cpu().numpy()), ref) <= TOL_BF16
+
+
+@pytest.mark.parametrize("hidden,inter", [(HIDDEN, INTER), (2048, 512)])
+def test_moe_decode_pool_norm(orc, dev, hidden, inter):
+    """Decode step + the next layer's input RMS norm (fused into the combine for
+    the 4096/1024 shape, a separate launch otherwise)."""
+    import torch
+    say("moe_decode_pool_norm", hidden, inter)
+    E, K = 16, 6
+    bits = [4 if e % 2 else 2 for e in range(E)]
+    blobs = experts(range(6000, 6000 + E), bits, hidden, inter)
+    pool = fm.DevicePool(blobs, bits, hidden, inter)
+    rng = synth.rng_for(22, hidden)
+    lg = rng.normal(0, 1, (1, E)).astype(np.float32)
+    x = synth.hidden_vec(rng, hidden)
+    hm = rng.normal(0, 1, hidden).astype(np.float32)
+    w = synth.bf16_bits(rng.normal(1, 0.2, hidden).astype(np.float32))
+    shared_blob = synth.expert_blob((6000, 99), hidden, inter, 4)
+    dsh = T(shared_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, hidden, inter)
+    idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+    wt = torch.empty((1, K), dtype=torch.float32, device=dev)
+    fm.route_topk(T(lg, dev), K, idx, wt)
+    ws = torch.empty(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    out = torch.empty(hidden, dtype=torch.float32, device=dev)
+    normed = torch.empty(hidden, dtype=torch.float32, device=dev)
+    for rep in range(2):  # a second call on the same workspace (stale tags must not leak)
+        fm.moe_decode_pool_norm(pool, idx, wt, T(x, dev), out, ws, T(w.view(np.int16), dev), 1e-6, normed,
+                                shared=sh, shared_bits=4, shared_score=T(np.array([0.2], np.float32), dev),
+                                h_mid=T(hm, dev))
+        torch.cuda.synchronize()
+        got_out = out.cpu().numpy()
+        assert norm_err(normed.cpu().numpy(), orc.rms_norm(got_out, w, 1e-6)) <= 1e-5
+    ri, rw = orc.route(lg, K)
+    ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], x, hidden, inter,
+                         shared_blob=shared_blob, shared_bits=4, shared_score=0.2, h_mid=hm)
+    assert norm_err(got_out - hm, ref - hm) <= TOL_F32
+    assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, w, 1e-6)) <= TOL_F32

@@ -56,6 +56,29 @@ def test_normalize_madd_bf16_golden(orc):
     assert np.array_equal(tr, GOLD["tr_out"])
 
 
+def test_rms_norm_golden(orc):
+    assert bits_eq(orc.rms_norm(GOLD["rn_x"], GOLD["rn_w"], float(GOLD["rn_eps"])), GOLD["rn_y"])
+
+
+def test_rms_norm_closed_form(orc):
+    """Constant x = c with unit weights: out = c / sqrt(c^2 + eps) (float64 check);
+    x and -x give mirrored outputs; scaling the weights scales the output."""
+    from fmoe_amd import synth
+    n, c, eps = 256, 3.0, 1e-5
+    x = np.full(n, c, np.float32)
+    w1 = synth.bf16_bits(np.ones(n, np.float32))
+    y = orc.rms_norm(x, w1, eps)
+    assert np.allclose(y, c / np.sqrt(c * c + eps), rtol=1e-6)
+    rng = synth.rng_for(77)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    w = synth.bf16_bits(rng.normal(1, 0.3, n).astype(np.float32))
+    assert bits_eq(orc.rms_norm(-x, w, eps), -orc.rms_norm(x, w, eps))
+    w2 = synth.bf16_bits(2 * synth.bf16_to_f32(w))  # exact doubling in bf16
+    assert bits_eq(orc.rms_norm(x, w2, eps), 2 * orc.rms_norm(x, w, eps))
+    ref64 = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps) * synth.bf16_to_f32(w)
+    assert np.max(np.abs(orc.rms_norm(x, w, eps) - ref64)) < 1e-5
+
+
 # ------------------------------------------------ live compiled reference ---
 def test_matvec4_vs_live_reference(orc, ref):
     rng = synth.rng_for(7)
