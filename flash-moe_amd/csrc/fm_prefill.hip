@@ -4,37 +4,39 @@
 // (batched_prefill.h:241-308) and only batches the shared expert / projections
 // with dequant_gemm_4bit_batch (shaders.metal:2140-2216, N <= 32 tokens).  Here
 // tokens are grouped by expert and every expert's weights stream once per 16
-// token columns through v_mfma_f32_16x16x32_f16:
+// tokens through v_mfma_f32_16x16x32_f16:
 //
 //   lists   routing idx -> per-expert entry lists + 16-entry chunks (device)
-//   gemm1   act[e,t] = silu(Wg x_t) * (Wu x_t)   for every (expert, token)
-//   gemm2   y[e,t]   = Wd act[e,t]               into the (token, slot) row
-//   combine out[t]   = h_mid + sum_k w_tk y[t,k] + sigmoid(g_t) y_shared[t]
-//                      in the slot order of batched_prefill.h:296-308
+//   ops     X -> fp16 token operands (pair layouts of both code widths) + sums
+//   gemm1   G[e,t] = Wg x_t, U[e,t] = Wu x_t          (separate blocks)
+//   ops     act = silu(G) * U -> token operands + sums
+//   gemm2   y[e,t] = Wd act[e,t]                       into the (token, slot) row
+//   combine out[t] = h_mid + sum_k w_tk y[t,k] + sigmoid(g_t) y_shared[t]
+//                    in the slot order of batched_prefill.h:296-308
 //
 // Exactness.  Weights never round: a masked 4-bit field with a zero fp16
 // exponent IS the fp16 subnormal code * 2^-24 (or * 2^-20), and MFMA consumes
 // fp16 subnormals exactly.  Each 64-element group accumulates in its own fp32
 // MFMA tile, then folds  acc += s_g * 2^24 * D_g + b_g * sum(x_g)  in fp32, as
-// the reference's per-group affine dequant requires.  Token activations enter
-// as fp16 hi (+ fp16 lo residual for fp32 inputs), pre-scaled to match the code
-// field positions; group sums come from the fp32 source.
+// the reference's per-group affine dequant requires.  Token inputs enter as
+// fp16 (bf16-exact hidden states; activations round like the decode path's)
+// pre-scaled to match the code field positions; plain fm_pfb_gemm adds an fp16
+// residual term for arbitrary fp32 inputs.  Group sums come from fp32.
 //
 // MFMA 16x16x32 operand layouts (gfx950): lane l holds A[l%16][8*(l/16)+0..7],
-// B[8*(l/16)+0..7][l%16], and D[4*(l/16)+v][l%16] for v = 0..3.  A = weight
-// rows (16 output features), B = 16 token columns, K = 32 codes per MFMA.
-// K order inside a group is a free permutation, chosen so each lane's 8 codes
-// come from one packed word (4-bit) or one half word (2-bit).
+// B[8*(l/16)+0..7][l%16], and D[4*(l/16)+v][l%16] for v = 0..3.  Here A = 16
+// token operands, B = 16 weight rows (codes), K = 32 codes per MFMA; a lane's
+// D values are 4 tokens of one row, so the fold needs one scale per lane.
 #include "fm_device.h"
 #include "fm_internal.h"
 
 typedef _Float16 fm_h8 __attribute__((ext_vector_type(8)));
 typedef float fm_f4v __attribute__((ext_vector_type(4)));
 
-#define PF_TOK 16          // token columns per chunk (one MFMA N tile)
-#define PF_FEAT_WAVE 64    // output features per wave (4 MFMA M tiles)
-#define PF_KB 8            // groups per LDS stage (512 inputs)
+#define PF_TOK 16    // token columns per MFMA N tile
+#define PF_CHUNK PF_TOK  // entries per chunk (one block covers a chunk x 64 rows)
 #define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: one fused decode step per token
+#define PF_TS 68     // words per row of a wave's transpose buffer (64 + 4 pad: no bank conflicts)
 
 // One expert's matrices.
 struct PfMat {
@@ -55,19 +57,22 @@ struct PfArgs {
     const uint32_t *pw;
     const uint16_t *ps, *pb;
     int pbits;
-    int mode;  // 0: gate/up + SwiGLU, 1: down -> y rows, 2: plain matrix -> Y rows
+    int mode;  // 0: gate and up -> G, U rows; 1: down -> y rows; 2: plain matrix -> Y rows
     // work lists
     const int *chunks;  // [max_chunks][4]: expert, entry offset, count, pad
     const int *nchunks;
     const int *entries;  // entry -> slot id
     int T, K;
     uint32_t max_chunks;
-    // B source rows (fp32): mode 0/2 -> X[token], mode 1 -> act[entry]
-    const float *src;
+    // B operands: per source row and group, 32 fp16 pairs in the 4-bit [0] and
+    // 2-bit [1] pair layouts (lo: residual terms, mode 2 only) + group sums.
+    // Source row: mode 0 token, mode 1 entry position, mode 2 token.
+    const fm_h2 *xop[2], *xlo[2];
+    const float *xsum;
     uint32_t in_dim, out_dim;
     // outputs
-    float *act;   // mode 0: [entries][inter]
-    float *y;     // mode 1: [slots][hidden]; mode 2: [T][out_dim]
+    float *gout, *uout;  // mode 0: [entries][inter]
+    float *y;            // mode 1: [slots][hidden]; mode 2: [T][out_dim]
 };
 
 __device__ __forceinline__ PfMat pf_mat(const PfArgs &a, int e, int which, int &bits) {
@@ -95,12 +100,12 @@ __device__ __forceinline__ PfMat pf_mat(const PfArgs &a, int e, int which, int &
     return m;
 }
 
-// slot -> B source row: token for X (mode 0/2), entry position for act (mode 1)
+// slot -> source row of the B operand: token for X (mode 0/2), entry position for act
 __device__ __forceinline__ int pf_token_of_slot(const PfArgs &a, int slot) {
     return slot < a.T * a.K ? slot / a.K : slot - a.T * a.K;
 }
 
-// A operand (8 fp16 subnormal codes) for a lane, from its packed word(s).
+// A operand (8 fp16 subnormal codes) for a lane, from its packed word.
 // 4-bit: one word w -> [c0 c4 c1' c5' c2 c6 c3' c7'] (' = *16 field)
 // 2-bit: half h of word w -> h=0: pairs n=0..3, h=1: pairs n=4..7
 template <int BITS>
@@ -126,241 +131,318 @@ __device__ __forceinline__ fm_h8 pf_codes(uint32_t w, int h) {
             r3 = t & 0x00300030u;
         }
     }
-    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-    u4v v = {r0, r1, r2, r3};
+    fm_u4 v = {r0, r1, r2, r3};
     return __builtin_bit_cast(fm_h8, v);
 }
 
-// LDS stage for one K-block of PF_KB groups:
-//  hi/lo  token operands: for each of PF_TOK tokens and PF_KB groups the 64
-//         inputs laid out [h=0..1][lane chunk c=0..3][8 halves] to match
-//         pf_codes, with the 2^-k field scales applied (fp16 hi + fp16 lo);
-//  psum   partial fp32 sums per (token, group, slot) -> sum per (token, group);
-//  sc     bf16 scales/biases of the block's 256 rows: [m][s|b][group][row].
+// ---------------------------------------------------------------- operands -
+// One 64-element group of a source row -> its B-operand pairs in both code
+// layouts (4-bit words: (x_j, x_{j+4}) * (j odd ? 2^-4 : 1); 2-bit words:
+// (x_n, x_{n+8}) / 4^(field of n)), optional residual terms, and the group
+// sum.  Four threads per group, 16 elements each.
+__global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict__ src, const float *__restrict__ src2,
+                                                        const int *__restrict__ nrows_dev, int nrows_max,
+                                                        uint32_t in_dim, fm_h2 *x4, fm_h2 *x2, fm_h2 *l4, fm_h2 *l2,
+                                                        float *xsum) {
+    const uint32_t G = in_dim / 64;
+    const uint32_t q = blockIdx.x * 256 + threadIdx.x;  // (row, group, quarter)
+    const int nrows = nrows_dev ? *nrows_dev : nrows_max;
+    const uint32_t row = q / (4 * G), g = (q / 4) % G, qq = q & 3;
+    const bool live = row < (uint32_t)nrows;
+    float v[16];
+    if (live) {
+        const float *xp = src + (size_t)row * in_dim + 64 * g + 16 * qq;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const fm_f4 t = fm_ldg_f4(xp + 4 * j);
+            v[4 * j] = t.x;
+            v[4 * j + 1] = t.y;
+            v[4 * j + 2] = t.z;
+            v[4 * j + 3] = t.w;
+        }
+        if (src2) {  // SwiGLU of separately computed gate and up rows
+            const float *up = src2 + (size_t)row * in_dim + 64 * g + 16 * qq;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const fm_f4 t = fm_ldg_f4(up + 4 * j);
+                v[4 * j] = fm_silu_mul(v[4 * j], t.x);
+                v[4 * j + 1] = fm_silu_mul(v[4 * j + 1], t.y);
+                v[4 * j + 2] = fm_silu_mul(v[4 * j + 2], t.z);
+                v[4 * j + 3] = fm_silu_mul(v[4 * j + 3], t.w);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = 0.f;
+    }
+    const size_t base = ((size_t)row * G + g) * 32;
+    const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float m = (j & 1) ? 0.0625f : 1.f;
+            const float a = v[8 * h + j] * m, b = v[8 * h + 4 + j] * m;
+            const fm_h2 hi = fm_pack_h2(a, b);
+            const size_t o = base + 4 * (2 * qq + h) + j;
+            if (live) {
+                x4[o] = hi;
+                if (l4) l4[o] = fm_pack_h2(a - (float)hi.x, b - (float)hi.y);
+            }
+        }
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const float a = v[n] * mt[n], b = v[8 + n] * mt[n];
+        const fm_h2 hi = fm_pack_h2(a, b);
+        const size_t o = base + 8 * qq + n;
+        if (live) {
+            x2[o] = hi;
+            if (l2) l2[o] = fm_pack_h2(a - (float)hi.x, b - (float)hi.y);
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (live && qq == 0) xsum[(size_t)row * G + g] = s;
+}
+
+// ---------------------------------------------------------------- gemm -----
+// One block = 4 waves = 64 rows (16 per wave) of ONE matrix x one chunk of <=
+// 16 entries of one expert.  The input dimension is walked in pieces of 8
+// groups:
+//  * weights stream row-contiguously (4-bit: load j gives lane l words
+//    4(l%16) .. +3 of row 4j + l/16, four 256-byte row runs per instruction;
+//    2-bit: 8 rows x 128 bytes per instruction) into a register ring
+//    PF_AHEAD pieces deep, together with each lane's scale/bias run of its row
+//    (lane l%16 = row), and pass through the wave's LDS transpose buffer into
+//    MFMA operand layout;
+//  * the chunk's token operands (pre-converted fp16 pairs, 128 bytes per token
+//    and group) and group sums are staged in LDS by the whole block, double
+//    buffered, loaded one piece ahead: one barrier per piece.
+// MFMA (src0 = tokens, src1 = codes): for group g, MFMA h takes in k slot kq
+// the word 2kq + h of the group (4-bit) or half h of word kq (2-bit); the token
+// operand holds the matching pairs (16(2kq + h) bytes into the group's 128-byte
+// pair block).  D[token = 4q + v][row = l%16], folded per group:
+//   acc_v += s_g * 2^24 * D_v + b_g * sum(x_g of token 4q + v).
+#define PF_GPP 8    // groups per piece
+#ifndef PF_AHEAD
+#define PF_AHEAD 2  // pieces of weights in flight beyond the one being computed
+#endif
+#ifndef PF_BPC
+#define PF_BPC 2
+#endif
+#define PF_XS (PF_GPP * 32 + 4)  // pairs per token row of the stage (+4: no LDS bank conflicts)
+#ifndef FM_PF_MARK
+#define FM_PF_MARK(n)
+#endif
+
+template <bool LO>
 struct PfStage {
-    _Float16 hi[PF_TOK][PF_KB][64];
-    _Float16 lo[PF_TOK][PF_KB][64];
-    float psum[PF_TOK][PF_KB][8];
-    float sum[PF_TOK][PF_KB];
-    uint16_t sc[2][2][PF_KB][256];
+    fm_h2 xop[LO ? 2 : 1][PF_TOK][PF_XS];
+    float xsum[PF_GPP][PF_TOK];
 };
 
-// Fill: task = (token, group, j), j = 0..7 one 8-half operand slot
-// (h = j / 4, c = j % 4) whose inputs are two float4 runs of the source row.
-template <int BITS, bool LO>
-__device__ void pf_stage_fill(PfStage &st, const float *src, const int *rows, int nrows, uint32_t in_dim, int g0,
-                              const PfMat *mats, int nm, int rblk, uint32_t out_dim) {
-    const uint32_t G = in_dim / 64;
-    for (int task = threadIdx.x; task < PF_TOK * PF_KB * 8; task += blockDim.x) {
-        const int j = task & 7, gg = (task >> 3) % PF_KB, tk = task / (8 * PF_KB);
-        const int h = j >> 2, c = j & 3;
-        const int g = g0 + gg;
-        const bool live = tk < nrows && (uint32_t)g < G;
-        fm_f4 va = {0.f, 0.f, 0.f, 0.f}, vb = {0.f, 0.f, 0.f, 0.f};
-        int base_a, base_b;
-        float sc[8];
-        if constexpr (BITS == 4) {
-            // word 2c + h: elements 8w .. 8w+7, pairs (n, n+4), n = 0..3; odd n carry 2^-4
-            base_a = 8 * (2 * c + h);
-            base_b = base_a + 4;
-            const float m[8] = {1.f, 1.f, 0.0625f, 0.0625f, 1.f, 1.f, 0.0625f, 0.0625f};
-#pragma unroll
-            for (int q = 0; q < 8; q++) sc[q] = m[q];
-        } else {
-            // word c, pairs n = 4h..4h+3: elements 16c + n and 16c + 8 + n
-            base_a = 16 * c + 4 * h;
-            base_b = base_a + 8;
-            const float mm[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
-#pragma unroll
-            for (int q = 0; q < 8; q++) sc[q] = mm[4 * h + (q >> 1)];
-        }
-        if (live) {
-            const float *x = src + (size_t)rows[tk] * in_dim + 64 * g;
-            va = fm_ldg_f4(x + base_a);
-            vb = fm_ldg_f4(x + base_b);
-        }
-        // operand order: (a0, b0, a1, b1, a2, b2, a3, b3)
-        const float v[8] = {va.x, vb.x, va.y, vb.y, va.z, vb.z, va.w, vb.w};
-        _Float16 *dh = &st.hi[tk][gg][j * 8];
-        _Float16 *dl = &st.lo[tk][gg][j * 8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const float xs = v[q] * sc[q];
-            const _Float16 vh = (_Float16)xs;
-            dh[q] = vh;
-            if (LO) dl[q] = (_Float16)(xs - (float)vh);
-        }
-        st.psum[tk][gg][j] = ((va.x + va.y) + (va.z + va.w)) + ((vb.x + vb.y) + (vb.z + vb.w));
-    }
-    // scales/biases of the block's rows for these groups
-    for (int task = threadIdx.x; task < nm * 2 * 256; task += blockDim.x) {
-        const int row = task & 255, sb = (task >> 8) & 1, m = task >> 9;
-        const int frow = min(rblk + row, (int)out_dim - 1);
-        const uint16_t *p = (sb ? mats[m].b : mats[m].s) + (size_t)frow * G + g0;
-#pragma unroll
-        for (int gg = 0; gg < PF_KB; gg++) st.sc[m][sb][gg][row] = (uint32_t)(g0 + gg) < G ? fm_ldg_u16(p + gg) : 0;
-    }
-    __syncthreads();
-    for (int task = threadIdx.x; task < PF_TOK * PF_KB; task += blockDim.x) {
-        const int gg = task % PF_KB, tk = task / PF_KB;
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) s += st.psum[tk][gg][j];
-        st.sum[tk][gg] = s;
-    }
-}
+template <bool LO>
+struct PfStageRegs {
+    fm_u4 x[LO ? 8 : 4];
+    float xs;
+};
 
 template <int BITS>
-__device__ __forceinline__ uint64_t pf_load_w(const PfMat &m, int row, uint32_t wpr, uint32_t g, int c) {
-    if constexpr (BITS == 4) {
-        return *(const FM_GLOBAL uint64_t *)(m.w + (size_t)row * wpr + 8 * g + 2 * c);
-    } else {
-        return *(const FM_GLOBAL uint32_t *)(m.w + (size_t)row * wpr + 4 * g + c);
-    }
-}
+struct PfPiece {
+    fm_u4 c[BITS == 4 ? 4 : 2];
+    fm_u4 s, b;  // this lane's row: scales / biases of the piece's 8 groups
+};
 
-template <int BITS, bool LO, bool GU>
-__device__ void pf_gemm_body(const PfArgs &a, PfStage &st, const int *rows, int nrows, const PfMat *mats, int rblk,
-                             int r0, fm_f4v (&acc)[2][4]) {
-    const int lane = threadIdx.x & 63;
-    const int c = lane >> 4, col = lane & 15;
-    const uint32_t G = a.in_dim / 64;
-    const uint32_t wpr = a.in_dim * BITS / 32;
-    constexpr int NM = GU ? 2 : 1;
-    const int wrow0 = r0 - rblk;  // this wave's first row within the block's 256
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) acc[m][t] = (fm_f4v){0.f, 0.f, 0.f, 0.f};
-    int arow[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) arow[t] = min(r0 + 16 * t + (lane & 15), (int)a.out_dim - 1);
-
-    uint64_t wcur[NM][4], wnxt[NM][4];
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-        for (int t = 0; t < 4; t++) wcur[m][t] = pf_load_w<BITS>(mats[m], arow[t], wpr, 0, c);
-
-    for (uint32_t g0 = 0; g0 < G; g0 += PF_KB) {
-        __syncthreads();
-        pf_stage_fill<BITS, LO>(st, a.src, rows, nrows, a.in_dim, g0, mats, NM, rblk, a.out_dim);
-        __syncthreads();
-        const int ng = min((int)PF_KB, (int)(G - g0));
-        for (int gg = 0; gg < ng; gg++) {
-            const uint32_t g = g0 + gg;
-            if (g + 1 < G) {
-#pragma unroll
-                for (int m = 0; m < NM; m++)
-#pragma unroll
-                    for (int t = 0; t < 4; t++) wnxt[m][t] = pf_load_w<BITS>(mats[m], arow[t], wpr, g + 1, c);
-            }
-            const fm_h8 bh0 = *(const fm_h8 *)&st.hi[col][gg][(0 * 4 + c) * 8];
-            const fm_h8 bh1 = *(const fm_h8 *)&st.hi[col][gg][(1 * 4 + c) * 8];
-            fm_h8 bl0, bl1;
-            if (LO) {
-                bl0 = *(const fm_h8 *)&st.lo[col][gg][(0 * 4 + c) * 8];
-                bl1 = *(const fm_h8 *)&st.lo[col][gg][(1 * 4 + c) * 8];
-            }
-            const float xs = st.sum[col][gg];
-#pragma unroll
-            for (int m = 0; m < NM; m++) {
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const uint64_t wv = wcur[m][t];
-                    const uint32_t w0 = (uint32_t)wv, w1 = BITS == 4 ? (uint32_t)(wv >> 32) : (uint32_t)wv;
-                    fm_f4v d = (fm_f4v){0.f, 0.f, 0.f, 0.f};
-                    const fm_h8 a0 = pf_codes<BITS>(w0, 0), a1 = pf_codes<BITS>(w1, 1);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh0, d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bh1, d, 0, 0, 0);
-                    if (LO) {
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bl0, d, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bl1, d, 0, 0, 0);
-                    }
-                    // fold rows 4c..4c+3 of tile t: s*2^24*D + b*sum(x)
-                    const int lr = wrow0 + 16 * t + 4 * c;
-                    const uint64_t s4 = *(const uint64_t *)&st.sc[m][0][gg][lr];
-                    const uint64_t b4 = *(const uint64_t *)&st.sc[m][1][gg][lr];
-#pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        const float sc = fm_bf16_to_f32((uint16_t)(s4 >> (16 * v))) * 16777216.0f;
-                        const float bi = fm_bf16_to_f32((uint16_t)(b4 >> (16 * v)));
-                        acc[m][t][v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs, acc[m][t][v]));
-                    }
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int t = 0; t < 4; t++) wcur[m][t] = wnxt[m][t];
-        }
-    }
-}
-
-// One block = 4 waves = 256 consecutive output features of one 16-entry chunk.
+// Branch-free stage loads (clamped addresses, zero by select) so the compiler
+// keeps every load of the next piece in flight during the current one.
 template <bool LO>
-__global__ __launch_bounds__(256) void fm_pf_gemm_kernel(PfArgs a) {
-    __shared__ PfStage st;
-    __shared__ int rows[PF_TOK];
-    __shared__ int slots[PF_TOK];
-    const uint32_t nfb = (a.out_dim + 255) / 256;
-    const uint32_t fb = blockIdx.x / a.max_chunks;
-    const uint32_t ci = blockIdx.x % a.max_chunks;
-    if ((int)ci >= *a.nchunks || fb >= nfb) return;
+__device__ __forceinline__ void pf_stage_load(const PfArgs &a, const int *srow, const fm_h2 *xop, const fm_h2 *xlo,
+                                              uint32_t g0, PfStageRegs<LO> &r) {
+    const int t = threadIdx.x;
+    const uint32_t G = a.in_dim / 64;
+#pragma unroll
+    for (int k = 0; k < (LO ? 8 : 4); k++) {
+        const int i = t + 256 * (k & 3);
+        const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
+        const int sr = srow[tok];
+        const uint32_t g = g0 + gg;
+        const bool ok = sr >= 0 && g < G;
+        const fm_h2 *base = k < 4 ? xop : xlo;
+        const fm_u4 v = *(const FM_GLOBAL fm_u4 *)(base + ((size_t)(ok ? sr : 0) * G + (ok ? g : 0)) * 32 + 4 * part);
+        r.x[k] = ok ? v : (fm_u4){0u, 0u, 0u, 0u};
+    }
+    const int tok = t & 15, gg = (t >> 4) & 7;
+    const int sr = srow[tok];
+    const bool ok = sr >= 0 && g0 + gg < G;
+    const float v = fm_ldg_f32(a.xsum + (size_t)(ok ? sr : 0) * G + (ok ? g0 + gg : 0));
+    r.xs = ok ? v : 0.f;
+}
+
+template <bool LO>
+__device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageRegs<LO> &r) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < (LO ? 8 : 4); k++) {
+        const int i = t + 256 * (k & 3);
+        const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
+        *(fm_u4 *)&st.xop[k >> 2][tok][32 * gg + 4 * part] = r.x[k];
+    }
+    if (t < PF_TOK * PF_GPP) st.xsum[(t >> 4) & 7][t & 15] = r.xs;
+}
+
+template <int BITS, bool LO>
+__device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *srow, PfStage<LO> (&st)[2],
+                         uint32_t *T, fm_f4v &acc) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, kq = lane >> 4;
+    const uint32_t G = a.in_dim / 64;
+    constexpr int WPG = 2 * BITS;     // words per group
+    constexpr int PW = PF_GPP * WPG;  // words per piece row (64 | 32)
+    constexpr int NL = PW / 16;       // loads per piece (4 | 2)
+    constexpr int RS = BITS == 4 ? 4 : 8;  // rows between a lane's loads
+    const uint32_t wpr = G * WPG;
+    const int np = (int)((G + PF_GPP - 1) / PF_GPP);
+    const fm_h2 *xop = a.xop[BITS == 4 ? 0 : 1];
+    const fm_h2 *xlo = a.xlo[BITS == 4 ? 0 : 1];
+    const int r0 = rb + 16 * wv;
+    acc = (fm_f4v){0.f, 0.f, 0.f, 0.f};
+    const int lrow = BITS == 4 ? kq : (lane >> 3);
+    const int lw = BITS == 4 ? 4 * n : 4 * (lane & 7);
+    const uint32_t *wrow[NL];
+#pragma unroll
+    for (int j = 0; j < NL; j++) wrow[j] = mat.w + (size_t)min(r0 + RS * j + lrow, (int)a.out_dim - 1) * wpr;
+    const int srow_r = min(r0 + n, (int)a.out_dim - 1);  // this lane's fold row
+    const uint16_t *sp = mat.s + (size_t)srow_r * G, *bp = mat.b + (size_t)srow_r * G;
+    const bool vec_sb = (G % PF_GPP) == 0;
+    auto load_piece = [&](int p, PfPiece<BITS> &d) {
+        const int pc = min(p, np - 1);  // past the end: re-read the last piece (no branch)
+        const uint32_t w = min((uint32_t)(PW * pc + lw), wpr - 4);
+#pragma unroll
+        for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(wrow[j] + w);
+        const uint32_t g0 = PF_GPP * pc;
+        if (vec_sb) {
+            d.s = *(const FM_GLOBAL fm_u4 *)(sp + g0);
+            d.b = *(const FM_GLOBAL fm_u4 *)(bp + g0);
+        } else {
+            uint32_t ws_[4] = {0u, 0u, 0u, 0u}, wb_[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int gg = 0; gg < PF_GPP; gg++) {
+                const uint32_t gi = min(g0 + gg, G - 1);
+                const uint32_t vs = fm_ldg_u16(sp + gi), vb = fm_ldg_u16(bp + gi);
+                ws_[gg >> 1] |= (g0 + gg < G ? vs : 0u) << (16 * (gg & 1));
+                wb_[gg >> 1] |= (g0 + gg < G ? vb : 0u) << (16 * (gg & 1));
+            }
+            d.s = (fm_u4){ws_[0], ws_[1], ws_[2], ws_[3]};
+            d.b = (fm_u4){wb_[0], wb_[1], wb_[2], wb_[3]};
+        }
+    };
+    PfPiece<BITS> ring[PF_AHEAD + 1];
+#pragma unroll
+    for (int k = 0; k <= PF_AHEAD; k++) load_piece(k, ring[k]);
+    PfStageRegs<LO> sr;
+    pf_stage_load<LO>(a, srow, xop, xlo, 0, sr);
+    pf_stage_store<LO>(st[0], sr);
+    __syncthreads();
+    FM_PF_MARK(1);
+    for (int p = 0; p < np; p++) {
+        PfStage<LO> &cs = st[p & 1];
+        const PfPiece<BITS> cur = ring[0];
+#pragma unroll
+        for (int k = 0; k < PF_AHEAD; k++) ring[k] = ring[k + 1];
+        load_piece(p + PF_AHEAD + 1, ring[PF_AHEAD]);
+        pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 1, np - 1) * PF_GPP, sr);
+        // transpose this wave's 16 rows of the piece through LDS
+#pragma unroll
+        for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
+        const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+#pragma unroll
+        for (int gg = 0; gg < PF_GPP; gg++) {
+            fm_h8 c0, c1;
+            if constexpr (BITS == 4) {
+                const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
+                c0 = pf_codes<4>((uint32_t)w2, 0);
+                c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
+            } else {
+                const uint32_t w = T[n * PF_TS + 4 * gg + kq];
+                c0 = pf_codes<2>(w, 0);
+                c1 = pf_codes<2>(w, 1);
+            }
+            const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
+            const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
+            fm_f4v d = {0.f, 0.f, 0.f, 0.f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, c0, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, c1, d, 0, 0, 0);
+            if constexpr (LO) {
+                const fm_h8 l0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq]);
+                const fm_h8 l1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq + 4]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, c0, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
+            }
+            const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
+            const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
+            const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
+            if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
+        }
+        if (p == 0) FM_PF_MARK(2);
+        if (p + 1 < np) pf_stage_store<LO>(st[(p + 1) & 1], sr);
+        __syncthreads();
+    }
+    FM_PF_MARK(3);
+}
+
+// grid: blockIdx = ((row block * nmat) + matrix) * max_chunks + chunk, so the
+// blocks that read the same weights for consecutive chunks run side by side
+template <bool LO>
+__global__ __launch_bounds__(256, LO ? 2 : PF_BPC) void fm_pf_gemm_kernel(PfArgs a) {
+    __shared__ PfStage<LO> st[2];
+    __shared__ uint32_t tbuf[4][16 * PF_TS];
+    __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t nmat = a.mode == 0 ? 2 : 1;
+    const uint32_t ci = blockIdx.x % a.max_chunks, rest = blockIdx.x / a.max_chunks;
+    const uint32_t mat = rest % nmat, rbk = rest / nmat;
+    if ((int)ci >= *a.nchunks) return;
+    FM_PF_MARK(0);
     const int *ch = a.chunks + 4 * ci;
     const int e = ch[0], off = ch[1], n = ch[2];
     if (threadIdx.x < PF_TOK) {
-        int sl = threadIdx.x < n ? a.entries[off + threadIdx.x] : 0;
-        slots[threadIdx.x] = sl;
-        if (a.mode == 1)
-            rows[threadIdx.x] = off + threadIdx.x;  // act row = entry position
-        else if (a.mode == 2)
-            rows[threadIdx.x] = sl;  // plain GEMM: entry = token row
-        else
-            rows[threadIdx.x] = pf_token_of_slot(a, sl);
+        const int ei = threadIdx.x;
+        int sl = -1, sr = -1;
+        if (ei < n) {
+            sl = a.entries[off + ei];
+            sr = a.mode == 1 ? off + ei : (a.mode == 2 ? sl : pf_token_of_slot(a, sl));
+        }
+        slot_s[ei] = sl;
+        srow_s[ei] = sr;
     }
     __syncthreads();
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r0 = fb * 256 + wv * PF_FEAT_WAVE;
-    int bits = 4, bits2 = 4;
-    PfMat mats[2];
-    if (a.mode == 0) {
-        mats[0] = pf_mat(a, e, 0, bits);
-        mats[1] = pf_mat(a, e, 1, bits2);
-    } else {
-        mats[0] = pf_mat(a, e, a.mode == 1 ? 2 : 0, bits);
-        mats[1] = mats[0];
-    }
-    fm_f4v acc[2][4];
-    const bool live = (uint32_t)r0 < a.out_dim;
-    const int rblk = fb * 256;
-    if (a.mode == 0) {
-        if (bits == 4)
-            pf_gemm_body<4, LO, true>(a, st, rows, n, mats, rblk, r0, acc);
-        else
-            pf_gemm_body<2, LO, true>(a, st, rows, n, mats, rblk, r0, acc);
-    } else {
-        if (bits == 4)
-            pf_gemm_body<4, LO, false>(a, st, rows, n, mats, rblk, r0, acc);
-        else
-            pf_gemm_body<2, LO, false>(a, st, rows, n, mats, rblk, r0, acc);
-    }
-    if (!live) return;
-    const int col = lane & 15, c = lane >> 4;
-    if (col >= n) return;
-    const int slot = slots[col];
+    int bits = 4;
+    const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), bits);
+    const int rb = rbk * 64;
+    fm_f4v acc;
+    uint32_t *T = tbuf[wv];
+    if (bits == 4)
+        pf_block<4, LO>(a, m, rb, srow_s, st, T, acc);
+    else
+        pf_block<2, LO>(a, m, rb, srow_s, st, T, acc);
+    // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + 16 wv + n
+    const int row = rb + 16 * wv + (lane & 15), q = lane >> 4;
+    if (row >= (int)a.out_dim) return;
+    float *dst = a.mode == 0 ? (mat == 0 ? a.gout : a.uout) : a.y;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const uint32_t f = r0 + 16 * t + 4 * c + v;
-            if (f >= a.out_dim) continue;
-            if (a.mode == 0) {
-                a.act[(size_t)(off + col) * a.out_dim + f] = fm_silu_mul(acc[0][t][v], acc[1][t][v]);
-            } else {
-                a.y[(size_t)slot * a.out_dim + f] = acc[0][t][v];
-            }
-        }
+    for (int v = 0; v < 4; v++) {
+        const int tk = 4 * q + v;
+        if (tk >= n) continue;
+        const size_t r = a.mode == 0 ? (size_t)(off + tk) : (size_t)slot_s[tk];
+        dst[r * a.out_dim + row] = acc[v];
+    }
+    FM_PF_MARK(4);
 }
 
 // ---------------------------------------------------------------- lists ----
@@ -394,7 +476,7 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             base[e] = acc;
             cbase[e] = cacc;
             acc += cnt[e];
-            cacc += (cnt[e] + PF_TOK - 1) / PF_TOK;
+            cacc += (cnt[e] + PF_CHUNK - 1) / PF_CHUNK;
         }
         base[NE] = acc;
         cbase[NE] = cacc;
@@ -405,12 +487,12 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     // chunks
     for (int e = threadIdx.x; e < NE; e += blockDim.x) {
         const int ne = cnt[e];
-        for (int j = 0; j * PF_TOK < ne; j++) {
+        for (int j = 0; j * PF_CHUNK < ne; j++) {
             const int ci = cbase[e] + j;
             if (ci >= (int)max_chunks) break;
             chunks[4 * ci + 0] = e;
-            chunks[4 * ci + 1] = base[e] + j * PF_TOK;
-            chunks[4 * ci + 2] = min(PF_TOK, ne - j * PF_TOK);
+            chunks[4 * ci + 1] = base[e] + j * PF_CHUNK;
+            chunks[4 * ci + 2] = min(PF_CHUNK, ne - j * PF_CHUNK);
             chunks[4 * ci + 3] = 0;
         }
     }
@@ -449,15 +531,39 @@ __global__ __launch_bounds__(256) void fm_pf_combine_kernel(const float *y, cons
 
 // ---------------------------------------------------------------- host -----
 static uint32_t pf_max_chunks(int T, int K, uint32_t E, int has_shared) {
-    // sum_e ceil(n_e / 16) <= min(E, T*K) + T*K / 16, plus the shared expert
+    // sum_e ceil(n_e / 64) <= min(E, T*K) + T*K / 64, plus the shared expert
     uint32_t n = (uint32_t)T * K;
-    uint32_t m = (n < E ? n : E) + n / PF_TOK + 1;
-    if (has_shared) m += (T + PF_TOK - 1) / PF_TOK;
+    uint32_t m = (n < E ? n : E) + n / PF_CHUNK + 1;
+    if (has_shared) m += (T + PF_CHUNK - 1) / PF_CHUNK;
     return m;
 }
 
+// B-operand block for `rows` source rows of in_dim inputs: pairs in both code
+// layouts (+ residual terms when lo), group sums.
+struct PfOps {
+    size_t x4, x2, l4, l2, sum, total;
+};
+
+static PfOps pf_ops_layout(size_t rows, uint32_t in_dim, bool lo, size_t o) {
+    PfOps P;
+    const size_t pairs = rows * (in_dim / 64) * 32 * sizeof(fm_h2);
+    P.x4 = o;
+    o += fm_align_up(pairs, 256);
+    P.x2 = o;
+    o += fm_align_up(pairs, 256);
+    P.l4 = lo ? o : 0;
+    if (lo) o += fm_align_up(pairs, 256);
+    P.l2 = lo ? o : 0;
+    if (lo) o += fm_align_up(pairs, 256);
+    P.sum = o;
+    o += fm_align_up(rows * (in_dim / 64) * sizeof(float), 256);
+    P.total = o;
+    return P;
+}
+
 struct PfLayout {
-    size_t entries, chunks, nchunks, err, act, y, total;
+    size_t entries, chunks, nchunks, err, gout, uout, y, total;
+    PfOps xo, ao;
 };
 
 static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t inter, int has_shared) {
@@ -473,10 +579,16 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     o += 256;
     L.err = o;
     o += 256;
-    L.act = o;
+    L.gout = o;
+    o += fm_align_up(nent * inter * 4, 256);
+    L.uout = o;
     o += fm_align_up(nent * inter * 4, 256);
     L.y = o;
     o += fm_align_up(nent * hidden * 4, 256);
+    L.xo = pf_ops_layout((size_t)T, hidden, false, o);
+    o = L.xo.total;
+    L.ao = pf_ops_layout(nent, inter, false, o);
+    o = L.ao.total;
     L.total = o;
     return L;
 }
@@ -486,9 +598,28 @@ extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_po
     return pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
 }
 
+static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,
+                         char *base, const PfOps &P, bool lo, hipStream_t st) {
+    const size_t threads = (size_t)nrows_max * (in_dim / 64) * 4;
+    hipLaunchKernelGGL(fm_pf_xop_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, src2, nrows_dev,
+                       nrows_max, in_dim, (fm_h2 *)(base + P.x4), (fm_h2 *)(base + P.x2),
+                       lo ? (fm_h2 *)(base + P.l4) : nullptr, lo ? (fm_h2 *)(base + P.l2) : nullptr,
+                       (float *)(base + P.sum));
+    return fm_check_launch("fm_pf_xop_kernel");
+}
+
+static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
+    a.xop[0] = (const fm_h2 *)(base + P.x4);
+    a.xop[1] = (const fm_h2 *)(base + P.x2);
+    a.xlo[0] = lo ? (const fm_h2 *)(base + P.l4) : nullptr;
+    a.xlo[1] = lo ? (const fm_h2 *)(base + P.l2) : nullptr;
+    a.xsum = (const float *)(base + P.sum);
+}
+
 static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
-    const uint32_t nfb = (a.out_dim + 255) / 256;
-    dim3 grid(nfb * a.max_chunks), block(256);
+    const uint32_t rowblocks = (a.out_dim + 63) / 64;
+    const uint32_t nmat = a.mode == 0 ? 2 : 1;
+    dim3 grid((unsigned)((size_t)a.max_chunks * rowblocks * nmat)), block(256);
     if (lo)
         hipLaunchKernelGGL(fm_pf_gemm_kernel<true>, grid, block, 0, st, a);
     else
@@ -535,9 +666,12 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
             return FM_OK;
         }
     }
+    if ((uintptr_t)X & 15) return fm_fail(FM_ERR_INVALID, "%s: X not 16-byte aligned", who);
+    if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     char *p = (char *)ws;
     hipStream_t st = fm_stream(stream);
     const uint32_t mc = pf_max_chunks(T, K, pool->num_experts, has_shared);
+    const size_t nent = (size_t)T * K + has_shared * T;
 
     // lists
     size_t lds = ((size_t)pool->num_experts * 3 + 5) * sizeof(int);
@@ -546,6 +680,9 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
                        has_shared, (int *)(p + L.entries), (int *)(p + L.chunks), (int *)(p + L.nchunks), mc,
                        (int *)(p + L.err));
     int rc = fm_check_launch("fm_pf_lists_kernel");
+    if (rc) return rc;
+    // token operands of X (hidden states are bf16-exact: fp16 hi only)
+    rc = pf_launch_ops(X, nullptr, nullptr, T, pool->hidden, p, L.xo, false, st);
     if (rc) return rc;
 
     PfArgs a = {};
@@ -575,24 +712,27 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     a.T = T;
     a.K = K;
     a.max_chunks = mc;
-    float *act = (float *)(p + L.act);
+    float *gout = (float *)(p + L.gout), *uout = (float *)(p + L.uout);
     float *y = (float *)(p + L.y);
 
-    // gemm1: gate/up + SwiGLU (hidden states are bf16-exact: hi only)
+    // gemm1: gate and up rows -> G, U [entry][inter] fp32
     a.mode = 0;
-    a.src = X;
+    pf_bind_ops(a, p, L.xo, false);
     a.in_dim = pool->hidden;
     a.out_dim = pool->inter;
-    a.act = act;
+    a.gout = gout;
+    a.uout = uout;
     rc = pf_launch_gemm(a, false, st);
     if (rc) return rc;
-    // gemm2: down projection of the fp32 activations (hi + lo)
+    // act = silu(G) * U as fp16 token operands, then gemm2 (down projection)
+    rc = pf_launch_ops(gout, uout, nullptr, (int)nent, pool->inter, p, L.ao, false, st);
+    if (rc) return rc;
     a.mode = 1;
-    a.src = act;
+    pf_bind_ops(a, p, L.ao, false);
     a.in_dim = pool->inter;
     a.out_dim = pool->hidden;
     a.y = y;
-    rc = pf_launch_gemm(a, true, st);
+    rc = pf_launch_gemm(a, false, st);
     if (rc) return rc;
     // combine
     dim3 cg((pool->hidden + 255) / 256, T);
@@ -602,25 +742,28 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
 }
 
 // ---------------------------------------------------------------- pfb gemm -
-// Y[N, out] = X[N, in] dequant(W)^T, X fp32 (hi + lo), one "expert" whose
-// entry list is the identity.
+// Y[N, out] = X[N, in] dequant(W)^T, X fp32 (fp16 hi + lo terms), one
+// "expert" whose entry list is the identity.
 __global__ void fm_pfb_lists_kernel(int N, int *entries, int *chunks, int *nchunks) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < N) entries[i] = i;
-    const int nc = (N + PF_TOK - 1) / PF_TOK;
+    const int nc = (N + PF_CHUNK - 1) / PF_CHUNK;
     if (i < nc) {
         chunks[4 * i + 0] = 0;
-        chunks[4 * i + 1] = i * PF_TOK;
-        chunks[4 * i + 2] = min(PF_TOK, N - i * PF_TOK);
+        chunks[4 * i + 1] = i * PF_CHUNK;
+        chunks[4 * i + 2] = min(PF_CHUNK, N - i * PF_CHUNK);
         chunks[4 * i + 3] = 0;
     }
     if (i == 0) *nchunks = nc;
 }
 
-extern "C" size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim) {
-    (void)in_dim;
-    const size_t nc = (N + PF_TOK - 1) / PF_TOK;
+static size_t pfb_head(uint32_t N) {
+    const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
     return fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * 16, 256) + 256;
+}
+
+extern "C" size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim) {
+    return pf_ops_layout(N, in_dim, true, pfb_head(N)).total;
 }
 
 extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases, const float *X, float *Y,
@@ -634,15 +777,20 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     FM_REQUIRE(N >= 1, "%s: N=%u", who, N);
     const size_t need = fm_pfb_gemm_workspace_size(N, in_dim);
     if (!ws || ws_bytes < need) return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu < %zu", who, ws_bytes, need);
+    if ((uintptr_t)X & 15) return fm_fail(FM_ERR_INVALID, "%s: X not 16-byte aligned", who);
+    if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     char *p = (char *)ws;
     int *entries = (int *)p;
     int *chunks = (int *)(p + fm_align_up((size_t)N * 4, 256));
-    const size_t nc = (N + PF_TOK - 1) / PF_TOK;
+    const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
     int *nchunks = (int *)(p + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * 16, 256));
     hipStream_t st = fm_stream(stream);
     const uint32_t nt = (uint32_t)(N > nc ? N : nc);
     hipLaunchKernelGGL(fm_pfb_lists_kernel, dim3((nt + 255) / 256), dim3(256), 0, st, (int)N, entries, chunks, nchunks);
     rc = fm_check_launch("fm_pfb_lists_kernel");
+    if (rc) return rc;
+    const PfOps P = pf_ops_layout(N, in_dim, true, pfb_head(N));
+    rc = pf_launch_ops(X, nullptr, nullptr, (int)N, in_dim, p, P, true, st);
     if (rc) return rc;
     PfArgs a = {};
     a.mode = 2;
@@ -656,7 +804,7 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     a.T = (int)N;
     a.K = 1;
     a.max_chunks = (uint32_t)nc;
-    a.src = X;
+    pf_bind_ops(a, p, P, true);
     a.in_dim = in_dim;
     a.out_dim = out_dim;
     a.y = Y;
