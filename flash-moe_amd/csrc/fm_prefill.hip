@@ -405,9 +405,14 @@ __global__ __launch_bounds__(256, LO ? 2 : PF_BPC) void fm_pf_gemm_kernel(PfArgs
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t nmat = a.mode == 0 ? 2 : 1;
-    const uint32_t ci = blockIdx.x % a.max_chunks, rest = blockIdx.x / a.max_chunks;
+    // XCD-aware order: the 8 XCDs take blocks round-robin, so give XCD x a
+    // contiguous range of units -- the chunks of one expert (consecutive units)
+    // then share that XCD's L2 instead of fetching the weights once per XCD.
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t ci = u % a.max_chunks, rest = u / a.max_chunks;
     const uint32_t mat = rest % nmat, rbk = rest / nmat;
-    if ((int)ci >= *a.nchunks) return;
+    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + 63) / 64) return;
     FM_PF_MARK(0);
     const int *ch = a.chunks + 4 * ci;
     const int e = ch[0], off = ch[1], n = ch[2];
@@ -619,7 +624,9 @@ static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
 static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     const uint32_t rowblocks = (a.out_dim + 63) / 64;
     const uint32_t nmat = a.mode == 0 ? 2 : 1;
-    dim3 grid((unsigned)((size_t)a.max_chunks * rowblocks * nmat)), block(256);
+    // whole multiple of 8 blocks (the XCD-aware unit order); extra units exit
+    const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
+    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(256);
     if (lo)
         hipLaunchKernelGGL(fm_pf_gemm_kernel<true>, grid, block, 0, st, a);
     else
