@@ -36,8 +36,12 @@
 #define FM_RT_NW (FM_RT_THREADS / 64)
 #define FM_RT_UMAX 256  // capacity of U (initial + inserted elements)
 #define FM_RT_MAXE 4096
+#ifndef FM_RT_MAX_PASSES
 #define FM_RT_MAX_PASSES (24 * FM_RT_NW)  // above this the serial replay is cheaper
+#endif
 #define FM_RT_VPT (FM_RT_MAXE / FM_RT_THREADS)  // logits per thread
+#define FM_RT_SMALL_NCH 16                      // chunks of the one-element-per-thread path
+#define FM_RT_FEW 8                             // survivors of a chunk tested with ballots
 #ifndef FM_RT_MARK
 #define FM_RT_MARK(n)
 #define FM_RT_DECL
@@ -57,6 +61,11 @@ struct FmRouteLds {
     int M, tie;
     int s_id[64];
     float s_val[64];
+    // E <= 64 * FM_RT_SMALL_NCH path
+    int big[FM_RT_SMALL_NCH][68] __attribute__((aligned(16)));  // chunk values >= its kth bound, -2 padded
+    int nbig[FM_RT_SMALL_NCH];
+    int c0cnt[64];                                              // chunk 0: #{j < i : p_j >= p_i}
+    int sv[FM_RT_NW][64] __attribute__((aligned(16)));          // per-wavefront survivors in lane order, -2 padded
 };
 
 FM_DEV float fm_wave_max(float v) {
@@ -81,6 +90,15 @@ FM_DEV int fm_wave_max_i(int v) {
     return max(max(r0, r1), max(r2, r3));
 }
 
+FM_DEV int fm_wave_sum_i(int v) {
+    v += fm_dpp_i<0xB1>(v);
+    v += fm_dpp_i<0x4E>(v);
+    v += fm_dpp_i<0x124>(v);
+    v += fm_dpp_i<0x128>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+
 // Inclusive prefix sum across the wavefront.
 FM_DEV int fm_wave_incl_scan(int v) {
     const int lane = threadIdx.x & 63;
@@ -90,6 +108,36 @@ FM_DEV int fm_wave_incl_scan(int v) {
         if (lane >= d) v += o;
     }
     return v;
+}
+
+// Largest value with the low FM_RT_KTH_LOW bits clear that at least K lanes
+// reach: a lower bound of the wave's K-th largest (bitwise radix select over
+// the high bits; the low bits would only tighten the bound slightly).
+#define FM_RT_KTH_LOW 16
+FM_DEV int fm_kth_lower_bound(int x, int K) {
+    int res = 0;
+#pragma unroll
+    for (int b = 30; b >= FM_RT_KTH_LOW; b--) {
+        const int cand = res | (1 << b);
+        if (__builtin_popcountll(__ballot(x >= cand)) >= K) res = cand;
+    }
+    return res;
+}
+
+// Row-local (16-lane) DPP shift right by N; lanes without a source get `fill`.
+template <int N>
+FM_DEV int fm_row_shr(int v, int fill) {
+    return __builtin_amdgcn_update_dpp(fill, v, 0x110 + N, 0xF, 0xF, false);
+}
+
+FM_DEV int fm_mbcnt(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
+}
+
+FM_DEV void fm_wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Serial replay on wavefront 0 (fallback): exact for ties.  The K slot keys
@@ -135,10 +183,196 @@ __device__ void fm_topk_serial(const int *pb, int E, int K, FmRouteLds &L) {
     }
 }
 
+// Top-K slots for E <= 64 * FM_RT_SMALL_NCH, one element per thread
+// (wavefront w holds chunk w in pv), called by the whole workgroup once pb,
+// the per-chunk lower bounds kth[] and the lists big[] are in LDS.  The tests
+// are lane-parallel VALU counts (one CU scalar unit serves all 16
+// wavefronts, so per-element ballot chains would serialise there):
+//  - chunk 0 has no bound: c_i = #{j < i : p_j >= p_i} is summed over all
+//    wavefronts, wavefront w adding the four j in [4w, 4w+4);
+//  - wavefront c >= 1 tests its survivors p_i > L_c: an earlier element
+//    p_j >= p_i > L_c >= kth[c'] is in big[c'], and an element of the own
+//    chunk p_j >= p_i is itself a survivor, so both counts run over short lists.
+// When U (initial elements plus insertions) fits one wavefront, wavefront 0
+// then ranks U, inverts the ranks and pointer-jumps the eviction chains in
+// registers.  Returns false (uniformly) when U is larger than a wavefront and
+// the general path must finish the job.
+__device__ bool fm_route_small(const int *pb, int pv, int E, int K, int nch, FmRouteLds &L) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = tid >> 6;
+    // lane c of lb: L_c = max over c' < c of kth[c'] (-1 for chunk 0)
+    int lb = lane < nch - 1 ? L.kth[lane] : -1;
+    lb = max(lb, fm_row_shr<1>(lb, -1));
+    lb = max(lb, fm_row_shr<2>(lb, -1));
+    lb = max(lb, fm_row_shr<4>(lb, -1));
+    lb = max(lb, fm_row_shr<8>(lb, -1));
+    lb = fm_row_shr<1>(lb, -1);
+    {
+        const int q0 = pb[lane];
+        const int4 pj = *reinterpret_cast<const int4 *>(&pb[4 * wv]);
+        const int j0 = 4 * wv;
+        const int part = (lane > j0 && pj.x >= q0) + (lane > j0 + 1 && pj.y >= q0) + (lane > j0 + 2 && pj.z >= q0) +
+                         (lane > j0 + 3 && pj.w >= q0);
+        if (part) atomicAdd(&L.c0cnt[lane], part);
+    }
+    FM_RT_MARK(11);
+    const int c = wv;
+    const int lc = __builtin_amdgcn_readlane(lb, c & 15);
+    if (c >= 1 && c < nch) {
+        const uint64_t own = __ballot(pv > lc);  // padding (-2) never passes; i >= 64 >= K
+        const int ns = __builtin_popcountll(own);
+        if (ns > 0 && ns <= FM_RT_FEW) {
+            // few survivors: one ballot per (survivor, earlier chunk), earlier chunks held in registers
+            int q[FM_RT_SMALL_NCH];
+#pragma unroll
+            for (int j = 0; j < FM_RT_SMALL_NCH; j++)
+                if (j < c) q[j] = pb[j * 64 + lane];
+            uint64_t rest = own, insc = 0;
+            while (rest) {
+                int sl[4], v[4], cnt[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    sl[b] = rest ? __builtin_ctzll(rest) : 64;
+                    rest &= rest - 1;  // no-op on 0
+                    const int x = __builtin_amdgcn_readlane(pv, min(sl[b], 63));
+                    v[b] = sl[b] < 64 ? x : 0x7fffffff;
+                    const uint64_t lt = sl[b] < 64 ? (1ull << sl[b]) - 1ull : 0ull;
+                    cnt[b] = __builtin_popcountll(__ballot(pv >= v[b]) & lt);
+                }
+#pragma unroll
+                for (int j = 0; j < FM_RT_SMALL_NCH; j++)
+                    if (j < c) {
+#pragma unroll
+                        for (int b = 0; b < 4; b++) cnt[b] += __builtin_popcountll(__ballot(q[j] >= v[b]));
+                    }
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    if (sl[b] < 64 && cnt[b] < K) insc |= 1ull << sl[b];
+            }
+            if (lane == 0) L.ins[c] = insc;  // sole writer of chunk c
+        } else if (ns > 0) {
+            // many survivors: lane-parallel counts over the survivor list and the big[] lists
+            const bool mine = (own >> lane) & 1ull;
+            const int r = fm_mbcnt(own);  // survivors below this lane = list entries before its own
+            L.sv[c][mine ? r : ns + lane - r] = mine ? pv : -2;
+            const int nbv = L.nbig[lane & 15];
+            fm_wave_lds_sync();
+            // below = #{entries e : e < p_i}; an entry counts as p_j >= p_i iff it is not below
+            int below = 0, seen = 0;
+            // own chunk, survivors before lane i (list in lane order)
+            for (int k = 0; k < ns; k += 4) {
+                const int4 e = *reinterpret_cast<const int4 *>(&L.sv[c][k]);
+                below += (k < r ? (int)((unsigned)(e.x - pv) >> 31) : 1) + (k + 1 < r ? (int)((unsigned)(e.y - pv) >> 31) : 1) +
+                         (k + 2 < r ? (int)((unsigned)(e.z - pv) >> 31) : 1) + (k + 3 < r ? (int)((unsigned)(e.w - pv) >> 31) : 1);
+                seen += 4;
+            }
+            // earlier chunks: first 16 entries of each list, next row prefetched
+            int4 cur[4];
+#pragma unroll
+            for (int h = 0; h < 4; h++) cur[h] = *reinterpret_cast<const int4 *>(&L.big[0][4 * h]);
+            for (int cp = 0; cp < c; cp++) {
+                int4 nxt[4];
+                const int cn = min(cp + 1, c - 1);
+#pragma unroll
+                for (int h = 0; h < 4; h++) nxt[h] = *reinterpret_cast<const int4 *>(&L.big[cn][4 * h]);
+#pragma unroll
+                for (int h = 0; h < 4; h++)
+                    below += (int)(((unsigned)(cur[h].x - pv) >> 31) + ((unsigned)(cur[h].y - pv) >> 31) +
+                                   ((unsigned)(cur[h].z - pv) >> 31) + ((unsigned)(cur[h].w - pv) >> 31));
+                seen += 16;
+                const int n = __builtin_amdgcn_readlane(nbv, cp);
+                for (int k = 16; k < n; k += 4) {  // long lists (K > 12 or ties at the bound)
+                    const int4 e = *reinterpret_cast<const int4 *>(&L.big[cp][k]);
+                    below += (int)(((unsigned)(e.x - pv) >> 31) + ((unsigned)(e.y - pv) >> 31) +
+                                   ((unsigned)(e.z - pv) >> 31) + ((unsigned)(e.w - pv) >> 31));
+                    seen += 4;
+                }
+#pragma unroll
+                for (int h = 0; h < 4; h++) cur[h] = nxt[h];
+            }
+            const int cnt = seen - below;
+            const uint64_t insc = __ballot(mine && cnt < K);
+            if (lane == 0) L.ins[c] = insc;  // sole writer of chunk c
+        }
+    }
+    FM_RT_MARK(12);
+    __syncthreads();
+    FM_RT_MARK(7);
+    const uint64_t ins0 = __ballot(lane >= K && lane < E && L.c0cnt[lane] < K);
+    const uint64_t im = lane == 0 ? ins0 : lane < nch ? L.ins[lane] : 0ull;
+    if (tid == 0) L.ins[0] = ins0;  // for the general path (read after its next barrier)
+    const int cnt = __builtin_popcountll(im);
+    int incl = cnt;
+    incl += fm_row_shr<1>(incl, 0);
+    incl += fm_row_shr<2>(incl, 0);
+    incl += fm_row_shr<4>(incl, 0);
+    incl += fm_row_shr<8>(incl, 0);
+    const int M = __builtin_amdgcn_readlane(incl, 15);
+    const int NU = K + M;
+    if (NU > 64) return false;
+    // U in LDS: position u < K holds initial element u, insertions follow in index order
+    // (cross-lane reads stay outside lane-divergent code: an inactive lane's value is undefined there)
+    const int pre = __builtin_amdgcn_readlane(incl - cnt, c & 15);
+    if (c < nch) {
+        const uint64_t mc = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(im >> 32), c & 15) << 32) |
+                            (unsigned)__builtin_amdgcn_readlane((int)im, c & 15);
+        if ((mc >> lane) & 1ull) {
+            const int pos = K + pre + fm_mbcnt(mc);
+            L.U[pos] = c * 64 + lane;
+            L.Uv[pos] = pv;
+        }
+    }
+    if (wv == 0) {
+        if (lane < K) {
+            L.U[lane] = lane;
+            L.Uv[lane] = pv;
+        } else if (lane >= NU) {
+            L.Uv[lane] = 0x7fffffff;
+        }
+    }
+    __syncthreads();
+    FM_RT_MARK(3);
+    if (wv == 0) {
+        const bool valid = lane < NU;
+        const int vu = L.Uv[lane];
+        const int uu = L.U[lane];
+        // ascending rank; distinct values give a permutation of 0..NU-1
+        int r = 0;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int4 vw[8];
+#pragma unroll
+            for (int w = 0; w < 8; w++) vw[w] = *reinterpret_cast<const int4 *>(&L.Uv[32 * h + 4 * w]);
+#pragma unroll
+            for (int w = 0; w < 8; w++) r += (vw[w].x < vu) + (vw[w].y < vu) + (vw[w].z < vu) + (vw[w].w < vu);
+        }
+        FM_RT_MARK(9);
+        if (fm_wave_sum_i(valid ? r : 0) != NU * (NU - 1) / 2) {
+            fm_topk_serial(pb, E, K, L);  // equal probabilities inside U
+        } else {
+            if (valid) L.tor[r] = lane;
+            fm_wave_lds_sync();
+            // x_m (position K+m-1) evicts the slot of the element of rank m-1
+            int ptr = lane < K ? lane : (valid ? L.tor[lane - K] : lane);
+            // chains are shorter than 64: six doublings reach every root
+#pragma unroll
+            for (int round = 0; round < 6; round++) ptr = __builtin_amdgcn_ds_bpermute(ptr << 2, ptr);
+            FM_RT_MARK(10);
+            // the K largest (ranks M .. NU-1) are the final slots
+            if (valid && r >= M) {
+                L.s_id[ptr] = uu;
+                L.s_val[ptr] = __int_as_float(vu);
+            }
+        }
+    }
+    return true;
+}
+
 __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__restrict__ logits, int T, int E,
                                                                  int K, int *__restrict__ idx,
                                                                  float *__restrict__ wout) {
-    extern __shared__ int pb[];  // probability bits, padded with -2 to whole chunks
+    extern __shared__ __attribute__((aligned(16))) int pb[];  // probability bits, padded with -2 to whole chunks
     __shared__ FmRouteLds L;
     const int t = blockIdx.x;
     const int tid = threadIdx.x;
@@ -164,6 +398,7 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
     if (lane == 0) L.red[0][wv] = mx;
     if (tid < FM_RT_MAXE / 64) L.ins[tid] = 0ull;
     if (tid < FM_RT_UMAX) L.rank[tid] = 0;
+    if (tid < 64) L.c0cnt[tid] = 0;
     if (tid == 0) L.tie = 0;
     __syncthreads();
 #pragma unroll
@@ -190,169 +425,188 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
         else if (i < nch * 64)
             pb[i] = -2;
     }
-    __syncthreads();
     FM_RT_MARK(1);
-
-    // K-th largest of every full chunk but the last (bitwise radix select)
-    for (int c = wv; c < nch - 1; c += FM_RT_NW) {
-        const int x = pb[c * 64 + lane];
-        int res = 0;
-        for (int b = 30; b >= 0; b--) {
-            const int cand = res | (1 << b);
-            if (__builtin_popcountll(__ballot(x >= cand)) >= K) res = cand;
-        }
-        if (lane == 0) L.kth[c] = res;
-    }
-    __syncthreads();
-    // survivors of chunk c: i >= K with p_i > L_c = max_{c' < c} kth[c'] (no bound in chunk 0)
-    for (int c = wv; c < nch; c += FM_RT_NW) {
-        const int lb = c == 0 ? -1 : fm_wave_max_i(lane < c ? L.kth[lane] : -1);
-        const uint64_t m = __ballot(c * 64 + lane >= K && pb[c * 64 + lane] > lb);
-        if (lane == 0) L.smask[c] = m;
-    }
-    __syncthreads();
-    FM_RT_MARK(7);
-
-    // exact test c_i = #{j < i : p_j >= p_i} < K for every survivor, in
-    // batches of eight survivors of one chunk spread over all wavefronts; a
-    // batch of chunk c takes c+1 ballots per survivor.
-    {
-        const uint64_t cm = lane < nch ? L.smask[lane] : 0ull;
-        const int nb = (__builtin_popcountll(cm) + 7) >> 3;
-        const int incl = fm_wave_incl_scan(nb);
-        const int pre = incl - nb;
-        const int NB = __builtin_amdgcn_readlane(incl, 63);
-        // ballot passes the batches would take; a weak filter (K close to 64,
-        // long ascending runs) makes the serial replay the cheaper choice
-        const int passes = fm_wave_incl_scan(lane < nch ? nb * (lane + 1) : 0);
-        const bool too_much = __builtin_amdgcn_readlane(passes, 63) > FM_RT_MAX_PASSES;
-        if (too_much && tid == 0) L.tie = 1;
-        for (int g = too_much ? NB : wv; g < NB; g += FM_RT_NW) {
-            const int c = __builtin_ctzll(__ballot(lane < nch && g >= pre && g < incl));
-            const int r8 = (g - __builtin_amdgcn_readlane(pre, c)) * 8;
-            const uint64_t msk = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(cm >> 32), c) << 32) |
-                                 (unsigned)__builtin_amdgcn_readlane((int)cm, c);
-            const int p = pb[c * 64 + lane];
-            const int rk = __builtin_popcountll(msk & lt_mask);
-            const bool mine = ((msk >> lane) & 1ull) && rk >= r8 && rk < r8 + 8;
-            int jb[8], pv[8], cnt[8];
-#pragma unroll
-            for (int b = 0; b < 8; b++) {
-                const uint64_t bm = __ballot(mine && rk == r8 + b);
-                jb[b] = bm ? __builtin_ctzll(bm) : 64;
-                pv[b] = bm ? __builtin_amdgcn_readlane(p, jb[b]) : 0x7fffffff;
-                cnt[b] = 0;
+    bool done = false;
+    if (nch <= FM_RT_SMALL_NCH) {
+        // one element per thread: wavefront w holds chunk w in a register
+        const int pv = tid < E ? __float_as_int(v[0] * inv) : -2;
+        if (wv < nch - 1) {
+            // the bound, and the chunk's values at or above it (the only ones a later
+            // survivor, being above the bound, can be compared unfavourably with)
+            const int res = fm_kth_lower_bound(pv, K);
+            const uint64_t bm = __ballot(pv >= res);
+            const int n = __builtin_popcountll(bm);
+            const int below = fm_mbcnt(bm);  // members below this lane; the others pad from n on
+            L.big[wv][((bm >> lane) & 1ull) ? below : n + lane - below] = ((bm >> lane) & 1ull) ? pv : -2;
+            if (lane < 4) L.big[wv][64 + lane] = -2;
+            if (lane == 0) {
+                L.kth[wv] = res;
+                L.nbig[wv] = n;
             }
-            for (int jc = 0; jc < c; jc++) {
-                const int q = pb[jc * 64 + lane];
-#pragma unroll
-                for (int b = 0; b < 8; b++) cnt[b] += __builtin_popcountll(__ballot(q >= pv[b]));
-            }
-            uint64_t insm = 0;
-#pragma unroll
-            for (int b = 0; b < 8; b++) {
-                cnt[b] += __builtin_popcountll(__ballot(p >= pv[b] && lane < jb[b]));
-                if (jb[b] < 64 && cnt[b] < K) insm |= 1ull << jb[b];
-            }
-            if (lane == 0 && insm) atomicOr(&L.ins[c], insm);
-        }
-    }
-    __syncthreads();
-    FM_RT_MARK(2);
-
-    // U = [0..K-1, insertions in index order]
-    if (wv == 0) {
-        const int cnt = lane < nch ? __builtin_popcountll(L.ins[lane]) : 0;
-        const int incl = fm_wave_incl_scan(cnt);
-        if (lane < nch) L.cpre[lane] = incl - cnt;
-        if (lane == 63) L.M = incl;
-    }
-    if (tid < K) {
-        L.U[tid] = tid;
-        L.Uv[tid] = pb[tid];
-    }
-    __syncthreads();
-    const int M = L.M;
-    const int NU = K + M;
-    const bool par = NU <= FM_RT_UMAX;
-    if (par) {
-        for (int i = tid; i < nch * 64; i += FM_RT_THREADS) {
-            const unsigned long long mk = L.ins[i >> 6];
-            if ((mk >> (i & 63)) & 1ull) {
-                const int pos = K + L.cpre[i >> 6] + __builtin_popcountll(mk & ((1ull << (i & 63)) - 1ull));
-                L.U[pos] = i;
-                L.Uv[pos] = pb[i];
-            }
-        }
-        if (tid < 4) L.Uv[NU + tid] = 0x7fffffff;
-    }
-    __syncthreads();
-    bool serial = !par || L.tie != 0;
-    if (!serial) {
-        // rank sort of U (ascending value), four partial counts per element
-        const int u = tid & (FM_RT_UMAX - 1);
-        const int qtr = tid / FM_RT_UMAX;
-        const int seg = ((NU + 15) >> 4) << 2;
-        if (u < NU) {
-            const int x = L.Uv[u];
-            int r = 0, eq = 0;
-            const int w1 = min(NU, (qtr + 1) * seg);
-            for (int w = qtr * seg; w < w1; w += 4) {
-                const int4 vw = *reinterpret_cast<const int4 *>(&L.Uv[w]);
-                r += (vw.x < x) + (vw.y < x) + (vw.z < x) + (vw.w < x);
-                eq += (vw.x == x) + (vw.y == x) + (vw.z == x) + (vw.w == x);
-            }
-            if (u >= qtr * seg && u < w1) eq--;  // itself
-            if (r) atomicAdd(&L.rank[u], r);
-            if (eq) L.tie = 1;  // equal probabilities inside U: slot choice needs the replay
         }
         __syncthreads();
-        serial = L.tie != 0;
-        if (!serial) {
-            if (tid < NU) L.tor[L.rank[tid]] = tid;
-            __syncthreads();
-            FM_RT_MARK(3);
-            if (wv == 0) {
-                // parents: initial elements are roots; x_m (position K+m-1) -> rank m-1.
-                // Pointer jumping within one wavefront until every chain reaches its root.
-                for (int q = lane; q < NU; q += 64) L.ptr[q] = q < K ? q : L.tor[q - K];
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                for (int round = 0; round < 9; round++) {
-                    int nx[FM_RT_UMAX / 64];
-                    bool ch = false;
-#pragma unroll
-                    for (int q = 0; q < FM_RT_UMAX / 64; q++) {
-                        const int uu = lane + 64 * q;
-                        const int pu = uu < NU ? L.ptr[uu] : 0;
-                        nx[q] = uu < NU ? L.ptr[pu] : 0;
-                        ch |= nx[q] != pu;
-                    }
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                    if (!__ballot(ch)) break;
-#pragma unroll
-                    for (int q = 0; q < FM_RT_UMAX / 64; q++) {
-                        const int uu = lane + 64 * q;
-                        if (uu < NU) L.ptr[uu] = nx[q];
-                    }
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        FM_RT_MARK(6);
+        done = fm_route_small(pb, pv, E, K, nch, L);
+    } else {
+        __syncthreads();
+        // lower bound of the K-th largest of every full chunk but the last
+        for (int c = wv; c < nch - 1; c += FM_RT_NW) {
+            const int res = fm_kth_lower_bound(pb[c * 64 + lane], K);
+            if (lane == 0) L.kth[c] = res;
+        }
+        __syncthreads();
+        FM_RT_MARK(6);
+        // survivors of chunk c: i >= K with p_i > L_c = max_{c' < c} kth[c'] (no bound in chunk 0)
+        for (int c = wv; c < nch; c += FM_RT_NW) {
+            const int lb = c == 0 ? -1 : fm_wave_max_i(lane < c ? L.kth[lane] : -1);
+            const uint64_t m = __ballot(c * 64 + lane >= K && pb[c * 64 + lane] > lb);
+            if (lane == 0) L.smask[c] = m;
+        }
+        __syncthreads();
+        FM_RT_MARK(7);
+
+        // exact test c_i = #{j < i : p_j >= p_i} < K for every survivor, in
+        // batches of eight survivors of one chunk spread over all wavefronts; a
+        // batch of chunk c takes c+1 ballots per survivor.
+        {
+            const uint64_t cm = lane < nch ? L.smask[lane] : 0ull;
+            const int nb = (__builtin_popcountll(cm) + 7) >> 3;
+            const int incl = fm_wave_incl_scan(nb);
+            const int pre = incl - nb;
+            const int NB = __builtin_amdgcn_readlane(incl, 63);
+            // ballot passes the batches would take; a weak filter (K close to 64,
+            // long ascending runs) makes the serial replay the cheaper choice
+            const int passes = fm_wave_incl_scan(lane < nch ? nb * (lane + 1) : 0);
+            const bool too_much = __builtin_amdgcn_readlane(passes, 63) > FM_RT_MAX_PASSES;
+            if (too_much && tid == 0) L.tie = 1;
+            for (int g = too_much ? NB : wv; g < NB; g += FM_RT_NW) {
+                const int c = __builtin_ctzll(__ballot(lane < nch && g >= pre && g < incl));
+                const int r8 = (g - __builtin_amdgcn_readlane(pre, c)) * 8;
+                const uint64_t msk = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(cm >> 32), c) << 32) |
+                                     (unsigned)__builtin_amdgcn_readlane((int)cm, c);
+                const int p = pb[c * 64 + lane];
+                const int rk = __builtin_popcountll(msk & lt_mask);
+                const bool mine = ((msk >> lane) & 1ull) && rk >= r8 && rk < r8 + 8;
+                int jb[8], pv[8], cnt[8];
+    #pragma unroll
+                for (int b = 0; b < 8; b++) {
+                    const uint64_t bm = __ballot(mine && rk == r8 + b);
+                    jb[b] = bm ? __builtin_ctzll(bm) : 64;
+                    pv[b] = bm ? __builtin_amdgcn_readlane(p, jb[b]) : 0x7fffffff;
+                    cnt[b] = 0;
                 }
-                // survivors = the K largest (ranks M .. NU-1); slot = root of the chain
-                for (int r = M + lane; r < NU; r += 64) {
-                    const int uu = L.tor[r];
-                    const int slot = L.ptr[uu];
-                    L.s_id[slot] = L.U[uu];
-                    L.s_val[slot] = __int_as_float(L.Uv[uu]);
+                for (int jc = 0; jc < c; jc++) {
+                    const int q = pb[jc * 64 + lane];
+    #pragma unroll
+                    for (int b = 0; b < 8; b++) cnt[b] += __builtin_popcountll(__ballot(q >= pv[b]));
+                }
+                uint64_t insm = 0;
+    #pragma unroll
+                for (int b = 0; b < 8; b++) {
+                    cnt[b] += __builtin_popcountll(__ballot(p >= pv[b] && lane < jb[b]));
+                    if (jb[b] < 64 && cnt[b] < K) insm |= 1ull << jb[b];
+                }
+                if (lane == 0 && insm) atomicOr(&L.ins[c], insm);
+            }
+        }
+        __syncthreads();
+    }
+    FM_RT_MARK(2);
+    if (!done) {
+        // U = [0..K-1, insertions in index order]
+        if (wv == 0) {
+            const int cnt = lane < nch ? __builtin_popcountll(L.ins[lane]) : 0;
+            const int incl = fm_wave_incl_scan(cnt);
+            if (lane < nch) L.cpre[lane] = incl - cnt;
+            if (lane == 63) L.M = incl;
+        }
+        if (tid < K) {
+            L.U[tid] = tid;
+            L.Uv[tid] = pb[tid];
+        }
+        __syncthreads();
+        const int M = L.M;
+        const int NU = K + M;
+        const bool par = NU <= FM_RT_UMAX;
+        if (par) {
+            for (int i = tid; i < nch * 64; i += FM_RT_THREADS) {
+                const unsigned long long mk = L.ins[i >> 6];
+                if ((mk >> (i & 63)) & 1ull) {
+                    const int pos = K + L.cpre[i >> 6] + __builtin_popcountll(mk & ((1ull << (i & 63)) - 1ull));
+                    L.U[pos] = i;
+                    L.Uv[pos] = pb[i];
+                }
+            }
+            if (tid < 4) L.Uv[NU + tid] = 0x7fffffff;
+        }
+        __syncthreads();
+        bool serial = !par || L.tie != 0;
+        if (!serial) {
+            // rank sort of U (ascending value), four partial counts per element
+            const int u = tid & (FM_RT_UMAX - 1);
+            const int qtr = tid / FM_RT_UMAX;
+            const int seg = ((NU + 15) >> 4) << 2;
+            if (u < NU) {
+                const int x = L.Uv[u];
+                int r = 0, eq = 0;
+                const int w1 = min(NU, (qtr + 1) * seg);
+                for (int w = qtr * seg; w < w1; w += 4) {
+                    const int4 vw = *reinterpret_cast<const int4 *>(&L.Uv[w]);
+                    r += (vw.x < x) + (vw.y < x) + (vw.z < x) + (vw.w < x);
+                    eq += (vw.x == x) + (vw.y == x) + (vw.z == x) + (vw.w == x);
+                }
+                if (u >= qtr * seg && u < w1) eq--;  // itself
+                if (r) atomicAdd(&L.rank[u], r);
+                if (eq) L.tie = 1;  // equal probabilities inside U: slot choice needs the replay
+            }
+            __syncthreads();
+            serial = L.tie != 0;
+            if (!serial) {
+                if (tid < NU) L.tor[L.rank[tid]] = tid;
+                __syncthreads();
+                FM_RT_MARK(3);
+                if (wv == 0) {
+                    // parents: initial elements are roots; x_m (position K+m-1) -> rank m-1.
+                    // Pointer jumping within one wavefront until every chain reaches its root.
+                    for (int q = lane; q < NU; q += 64) L.ptr[q] = q < K ? q : L.tor[q - K];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    for (int round = 0; round < 9; round++) {
+                        int nx[FM_RT_UMAX / 64];
+                        bool ch = false;
+    #pragma unroll
+                        for (int q = 0; q < FM_RT_UMAX / 64; q++) {
+                            const int uu = lane + 64 * q;
+                            const int pu = uu < NU ? L.ptr[uu] : 0;
+                            nx[q] = uu < NU ? L.ptr[pu] : 0;
+                            ch |= nx[q] != pu;
+                        }
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        if (!__ballot(ch)) break;
+    #pragma unroll
+                        for (int q = 0; q < FM_RT_UMAX / 64; q++) {
+                            const int uu = lane + 64 * q;
+                            if (uu < NU) L.ptr[uu] = nx[q];
+                        }
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    }
+                    // survivors = the K largest (ranks M .. NU-1); slot = root of the chain
+                    for (int r = M + lane; r < NU; r += 64) {
+                        const int uu = L.tor[r];
+                        const int slot = L.ptr[uu];
+                        L.s_id[slot] = L.U[uu];
+                        L.s_val[slot] = __int_as_float(L.Uv[uu]);
+                    }
                 }
             }
         }
+        if (serial && wv == 0) fm_topk_serial(pb, E, K, L);
     }
-    if (serial && wv == 0) fm_topk_serial(pb, E, K, L);
     __syncthreads();
     FM_RT_MARK(4);
     // cpu_normalize_weights: sequential sum over slots, then scale by 1/sum

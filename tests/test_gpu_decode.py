@@ -57,7 +57,10 @@ def test_batch_matvec_mixed(orc, dev):
                                          (16, 64, 64, "normal"), (8, 10, 10, "normal"), (32, 128, 16, "dup"),
                                          (4, 4096, 8, "normal"), (3, 512, 20, "normal"),
                                          (64, 512, 10, "normal"), (4, 512, 10, "asc"), (4, 300, 16, "asc"),
-                                         (4, 512, 10, "desc"), (8, 4096, 64, "normal"), (16, 70, 7, "dup")])
+                                         (4, 512, 10, "desc"), (8, 4096, 64, "normal"), (16, 70, 7, "dup"),
+                                         (32, 1024, 16, "normal"), (16, 1000, 10, "normal"),
+                                         (16, 1025, 10, "normal"), (4, 1024, 10, "asc"), (64, 512, 32, "normal"),
+                                         (16, 65, 10, "normal"), (16, 960, 40, "zipf"), (16, 1024, 4, "dup")])
 def test_route_topk(orc, dev, Tn, E, K, kind):
     import torch
     say("route", Tn, E, K, kind)
