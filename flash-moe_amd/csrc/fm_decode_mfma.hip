@@ -169,6 +169,38 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
             return on ? xq_grp0 + 32 * m + 4 * i : zero;
         }
     };
+    if constexpr (BITS == 4) {
+        // A lane's operand is non-zero in 4 of the 32 steps only, always with
+        // pairs of its own group m: keep those 4 quads in registers and select
+        // per step (no LDS operand traffic in the loop).
+        fmm_h8 xv[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) xv[s] = fmm_lds_op(xq_grp0 + 32 * m + 16 * (kq & 1) + 4 * s);
+        const fmm_h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        const bool kq_on = (kq >> 1) == (m & 1);
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) *(fm_u4 *)&T[(4 * j + kq) * FMM_TS + 4 * m] = cd.c[4 * p + j];
+            fm_u4 v[4];
+#pragma unroll
+            for (int h = 0; h < 4; h++) v[h] = *(const fm_u4 *)&T[m * FMM_TS + 16 * h + 4 * kq];
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++) {
+                const int j = 16 * p + jj;
+                const int c = j >> 3, i = j & 7;
+                const bool on = kq_on && c == (m >> 2) && (i >> 2) == ((m >> 1) & 1);
+                const fmm_h8 xo = on ? xv[i & 3] : z;
+                const fmm_h8 co = fmm_codes<4>(fmm_comp(v[2 * (c & 1) + (i >> 2)], i & 3), 0);
+                if (i & 1)
+                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d1, 0, 0, 0);
+                else
+                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xo, co, d0, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        return;
+    }
     constexpr int NP = BITS == 4 ? 2 : 1;
     fmm_h8 xo = fmm_lds_op(src_of(0));
 #pragma unroll
