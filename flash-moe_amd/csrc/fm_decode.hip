@@ -23,6 +23,8 @@
 #include "fm_decode.h"
 
 #include <atomic>
+#include <stdlib.h>
+#include <string.h>
 
 #define FM_DECODE_BLOCKS_PER_CU 4  // persistent 256-thread blocks per CU (cap)
 
@@ -739,6 +741,13 @@ static int fm_launch_eager(FmDecodeArgs &a, int lh, int li, hipStream_t st) {
     return fm_fail(FM_ERR_UNSUPPORTED, "eager decode: lanes");
 }
 
+// FMOE_DECODE_KERNEL=mfma|eager|fused restricts the decode step to
+// one kernel family (tests and benchmarks compare them); unset = fastest that fits.
+static bool fm_decode_allowed(const char *name) {
+    static const char *only = getenv("FMOE_DECODE_KERNEL");
+    return !only || !*only || !strcmp(only, name);
+}
+
 static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const char *who = "fm_moe_decode";
     FM_REQUIRE(a.hidden % 64 == 0 && a.inter % 64 == 0 && a.hidden && a.inter,
@@ -759,9 +768,9 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     a.ss2 = (uint64_t *)p;
     a.epoch = fm_next_epoch();
     if (a.norm_w) {
-        // the fused kernel normalises in its combine; every other path runs
+        // the fused kernels normalise in their combine; every other path runs
         // the standalone norm after the step
-        int rc = fm_launch_decode_mfma(a, st);
+        int rc = fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st) : FM_ERR_UNSUPPORTED;
         if (rc != FM_ERR_UNSUPPORTED) return rc;
         fm_clear_error();
         FmDecodeArgs b = a;
@@ -776,11 +785,11 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     if (!fm_pick_lanes(a.hidden / 64, &lh, &gh) || !fm_pick_lanes(a.inter / 64, &li, &gi) || gh > 2 || gi > 2)
         return fm_fail(FM_ERR_UNSUPPORTED, "%s: hidden %u / inter %u must be <= 8192", who, a.hidden, a.inter);
     {
-        int rc = fm_launch_decode_mfma(a, st);
+        int rc = fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st) : FM_ERR_UNSUPPORTED;
         if (rc != FM_ERR_UNSUPPORTED) return rc;
         fm_clear_error();
     }
-    if (gh == 1 && gi == 1) {
+    if (gh == 1 && gi == 1 && fm_decode_allowed("eager")) {
         int rc = fm_launch_eager(a, lh, li, st);
         if (rc != FM_ERR_UNSUPPORTED) return rc;
         fm_clear_error();

@@ -289,3 +289,23 @@ def test_moe_decode_pool_norm(orc, dev, hidden, inter):
                          shared_blob=shared_blob, shared_bits=4, shared_score=0.2, h_mid=hm)
     assert norm_err(got_out - hm, ref - hm) <= TOL_F32
     assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, w, 1e-6)) <= TOL_F32
+
+
+def test_moe_decode_repeated_calls_one_workspace(orc, dev):
+    """Back-to-back decode steps on one workspace: each call's activation
+    hand-off must only see its own words (epoch tags), never the previous
+    call's, including when the slot count and bit widths change."""
+    import torch
+    say("moe_decode repeated calls")
+    ws = torch.zeros(fm.decode_workspace_bytes(11, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    for rep, (K, bl) in enumerate([(10, [4] * 11), (10, [2, 4] * 5 + [4]), (5, [4, 2, 2, 4, 4, 2]), (10, [4] * 11)]):
+        blobs, x, hm, w, score = _decode_inputs(500 + rep, K, bl)
+        dblobs = [T(b, dev) for b in blobs]
+        ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
+        fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, shared=ex[K], shared_bits=bl[K],
+                      shared_score=score, h_mid=T(hm, dev))
+        torch.cuda.synchronize()
+        ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, shared_blob=blobs[K], shared_bits=bl[K],
+                             shared_score=score, h_mid=hm)
+        assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, rep
