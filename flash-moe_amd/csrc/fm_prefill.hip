@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict_
 //  * weights stream row-contiguously (4-bit: load j gives lane l words
 //    4(l%16) .. +3 of row 4j + l/16, four 256-byte row runs per instruction;
 //    2-bit: 8 rows x 128 bytes per instruction) into a register ring
-//    PF_AHEAD pieces deep, together with each lane's scale/bias run of its row
+//    PF_RING pieces deep, together with each lane's scale/bias run of its row
 //    (lane l%16 = row), and pass through the wave's LDS transpose buffer into
 //    MFMA operand layout;
 //  * the chunk's token operands (pre-converted fp16 pairs, 128 bytes per token
@@ -227,13 +227,19 @@ __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict_
 // pair block).  D[token = 4q + v][row = l%16], folded per group:
 //   acc_v += s_g * 2^24 * D_v + b_g * sum(x_g of token 4q + v).
 #define PF_GPP 8    // groups per piece
-#ifndef PF_AHEAD
-#define PF_AHEAD 2  // pieces of weights in flight beyond the one being computed
-#endif
-#ifndef PF_BPC
-#define PF_BPC 2
+#ifndef PF_RING
+#define PF_RING 2   // pieces of weights in flight (static ring slots; even)
 #endif
 #define PF_XS (PF_GPP * 32 + 4)  // pairs per token row of the stage (+4: no LDS bank conflicts)
+#ifndef PF_W
+#define PF_W 4      // waves per block: 16 rows each, so a block covers 16 * PF_W rows
+#endif
+#ifndef PF_MINB
+#define PF_MINB 2   // blocks per CU the register budget is sized for
+#endif
+#define PF_NT (64 * PF_W)
+#define PF_ROWS (16 * PF_W)
+#define PF_KS (PF_TOK * PF_GPP * 8 / PF_NT)  // 16-byte stage pieces per thread and operand array
 #ifndef FM_PF_MARK
 #define FM_PF_MARK(n)
 #endif
@@ -246,7 +252,7 @@ struct PfStage {
 
 template <bool LO>
 struct PfStageRegs {
-    fm_u4 x[LO ? 8 : 4];
+    fm_u4 x[(LO ? 2 : 1) * PF_KS];
     float xs;
 };
 
@@ -264,13 +270,13 @@ __device__ __forceinline__ void pf_stage_load(const PfArgs &a, const int *srow, 
     const int t = threadIdx.x;
     const uint32_t G = a.in_dim / 64;
 #pragma unroll
-    for (int k = 0; k < (LO ? 8 : 4); k++) {
-        const int i = t + 256 * (k & 3);
+    for (int k = 0; k < (LO ? 2 : 1) * PF_KS; k++) {
+        const int i = t + PF_NT * (k % PF_KS);
         const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
         const int sr = srow[tok];
         const uint32_t g = g0 + gg;
         const bool ok = sr >= 0 && g < G;
-        const fm_h2 *base = k < 4 ? xop : xlo;
+        const fm_h2 *base = k < PF_KS ? xop : xlo;
         const fm_u4 v = *(const FM_GLOBAL fm_u4 *)(base + ((size_t)(ok ? sr : 0) * G + (ok ? g : 0)) * 32 + 4 * part);
         r.x[k] = ok ? v : (fm_u4){0u, 0u, 0u, 0u};
     }
@@ -285,15 +291,15 @@ template <bool LO>
 __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageRegs<LO> &r) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < (LO ? 8 : 4); k++) {
-        const int i = t + 256 * (k & 3);
+    for (int k = 0; k < (LO ? 2 : 1) * PF_KS; k++) {
+        const int i = t + PF_NT * (k % PF_KS);
         const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
-        *(fm_u4 *)&st.xop[k >> 2][tok][32 * gg + 4 * part] = r.x[k];
+        *(fm_u4 *)&st.xop[k / PF_KS][tok][32 * gg + 4 * part] = r.x[k];
     }
     if (t < PF_TOK * PF_GPP) st.xsum[(t >> 4) & 7][t & 15] = r.xs;
 }
 
-template <int BITS, bool LO>
+template <int BITS, bool LO, bool VEC>
 __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *srow, PfStage<LO> (&st)[2],
                          uint32_t *T, fm_f4v &acc) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, kq = lane >> 4;
@@ -315,14 +321,13 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *s
     for (int j = 0; j < NL; j++) wrow[j] = mat.w + (size_t)min(r0 + RS * j + lrow, (int)a.out_dim - 1) * wpr;
     const int srow_r = min(r0 + n, (int)a.out_dim - 1);  // this lane's fold row
     const uint16_t *sp = mat.s + (size_t)srow_r * G, *bp = mat.b + (size_t)srow_r * G;
-    const bool vec_sb = (G % PF_GPP) == 0;
     auto load_piece = [&](int p, PfPiece<BITS> &d) {
         const int pc = min(p, np - 1);  // past the end: re-read the last piece (no branch)
         const uint32_t w = min((uint32_t)(PW * pc + lw), wpr - 4);
 #pragma unroll
         for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(wrow[j] + w);
         const uint32_t g0 = PF_GPP * pc;
-        if (vec_sb) {
+        if constexpr (VEC) {  // G % PF_GPP == 0: the piece's 8 scales are one 16-byte run
             d.s = *(const FM_GLOBAL fm_u4 *)(sp + g0);
             d.b = *(const FM_GLOBAL fm_u4 *)(bp + g0);
         } else {
@@ -338,60 +343,73 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *s
             d.b = (fm_u4){wb_[0], wb_[1], wb_[2], wb_[3]};
         }
     };
-    PfPiece<BITS> ring[PF_AHEAD + 1];
+    // Ring of PF_RING pieces with static slots: the piece loop is unrolled by
+    // PF_RING, so no register ever moves between slots (a move would wait for
+    // the slot's loads) and every piece issues the same loads -- the in-order
+    // wait counts stay exact and PF_RING - 1 pieces stay in flight while one
+    // is computed.  Token stages: piece p + 1's registers are stored to LDS
+    // while piece p + 2's are already loading.
+    constexpr int R = PF_RING;
+    PfPiece<BITS> ring[R];
 #pragma unroll
-    for (int k = 0; k <= PF_AHEAD; k++) load_piece(k, ring[k]);
-    PfStageRegs<LO> sr;
-    pf_stage_load<LO>(a, srow, xop, xlo, 0, sr);
-    pf_stage_store<LO>(st[0], sr);
+    for (int k = 0; k < R; k++) load_piece(k, ring[k]);
+    PfStageRegs<LO> sr[2];
+    pf_stage_load<LO>(a, srow, xop, xlo, 0, sr[0]);
+    pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
+    pf_stage_store<LO>(st[0], sr[0]);
     __syncthreads();
     FM_PF_MARK(1);
-    for (int p = 0; p < np; p++) {
-        PfStage<LO> &cs = st[p & 1];
-        const PfPiece<BITS> cur = ring[0];
+    for (int p0 = 0; p0 < np; p0 += R) {
 #pragma unroll
-        for (int k = 0; k < PF_AHEAD; k++) ring[k] = ring[k + 1];
-        load_piece(p + PF_AHEAD + 1, ring[PF_AHEAD]);
-        pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 1, np - 1) * PF_GPP, sr);
-        // transpose this wave's 16 rows of the piece through LDS
+        for (int i = 0; i < R; i++) {
+            const int p = p0 + i;
+            if (p < np) {
+                pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 2, np - 1) * PF_GPP, sr[i & 1]);
+                PfStage<LO> &cs = st[i & 1];
+                const PfPiece<BITS> &cur = ring[i];
+                // transpose this wave's 16 rows of the piece through LDS
 #pragma unroll
-        for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
-        const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+                for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
+                __builtin_amdgcn_sched_barrier(0);
+                const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
+                const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
 #pragma unroll
-        for (int gg = 0; gg < PF_GPP; gg++) {
-            fm_h8 c0, c1;
-            if constexpr (BITS == 4) {
-                const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
-                c0 = pf_codes<4>((uint32_t)w2, 0);
-                c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
-            } else {
-                const uint32_t w = T[n * PF_TS + 4 * gg + kq];
-                c0 = pf_codes<2>(w, 0);
-                c1 = pf_codes<2>(w, 1);
+                for (int gg = 0; gg < PF_GPP; gg++) {
+                    fm_h8 c0, c1;
+                    if constexpr (BITS == 4) {
+                        const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
+                        c0 = pf_codes<4>((uint32_t)w2, 0);
+                        c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
+                    } else {
+                        const uint32_t w = T[n * PF_TS + 4 * gg + kq];
+                        c0 = pf_codes<2>(w, 0);
+                        c1 = pf_codes<2>(w, 1);
+                    }
+                    const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
+                    const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
+                    fm_f4v d = {0.f, 0.f, 0.f, 0.f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, c0, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, c1, d, 0, 0, 0);
+                    if constexpr (LO) {
+                        const fm_h8 l0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq]);
+                        const fm_h8 l1 =
+                            __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq + 4]);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, c0, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
+                    }
+                    const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
+                    const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
+                    const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
+                    if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
+                }
+                if (p == 0) FM_PF_MARK(2);
+                load_piece(p + R, ring[i]);
+                if (p + 1 < np) pf_stage_store<LO>(st[(i + 1) & 1], sr[(i + 1) & 1]);
+                __syncthreads();
             }
-            const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
-            const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
-            fm_f4v d = {0.f, 0.f, 0.f, 0.f};
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, c0, d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, c1, d, 0, 0, 0);
-            if constexpr (LO) {
-                const fm_h8 l0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq]);
-                const fm_h8 l1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq + 4]);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, c0, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
-            }
-            const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
-            const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
-            const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
-#pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
-            if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
         }
-        if (p == 0) FM_PF_MARK(2);
-        if (p + 1 < np) pf_stage_store<LO>(st[(p + 1) & 1], sr);
-        __syncthreads();
     }
     FM_PF_MARK(3);
 }
@@ -399,9 +417,9 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *s
 // grid: blockIdx = ((row block * nmat) + matrix) * max_chunks + chunk, so the
 // blocks that read the same weights for consecutive chunks run side by side
 template <bool LO>
-__global__ __launch_bounds__(256, LO ? 2 : PF_BPC) void fm_pf_gemm_kernel(PfArgs a) {
+__global__ __launch_bounds__(PF_NT, PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
     __shared__ PfStage<LO> st[2];
-    __shared__ uint32_t tbuf[4][16 * PF_TS];
+    __shared__ uint32_t tbuf[PF_W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t nmat = a.mode == 0 ? 2 : 1;
@@ -412,7 +430,7 @@ __global__ __launch_bounds__(256, LO ? 2 : PF_BPC) void fm_pf_gemm_kernel(PfArgs
     const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     const uint32_t ci = u % a.max_chunks, rest = u / a.max_chunks;
     const uint32_t mat = rest % nmat, rbk = rest / nmat;
-    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + 63) / 64) return;
+    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + PF_ROWS - 1) / PF_ROWS) return;
     FM_PF_MARK(0);
     const int *ch = a.chunks + 4 * ci;
     const int e = ch[0], off = ch[1], n = ch[2];
@@ -429,13 +447,21 @@ __global__ __launch_bounds__(256, LO ? 2 : PF_BPC) void fm_pf_gemm_kernel(PfArgs
     __syncthreads();
     int bits = 4;
     const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), bits);
-    const int rb = rbk * 64;
+    const int rb = rbk * PF_ROWS;
     fm_f4v acc;
     uint32_t *T = tbuf[wv];
-    if (bits == 4)
-        pf_block<4, LO>(a, m, rb, srow_s, st, T, acc);
-    else
-        pf_block<2, LO>(a, m, rb, srow_s, st, T, acc);
+    const bool vec = (a.in_dim / 64) % PF_GPP == 0;
+    if (bits == 4) {
+        if (vec)
+            pf_block<4, LO, true>(a, m, rb, srow_s, st, T, acc);
+        else
+            pf_block<4, LO, false>(a, m, rb, srow_s, st, T, acc);
+    } else {
+        if (vec)
+            pf_block<2, LO, true>(a, m, rb, srow_s, st, T, acc);
+        else
+            pf_block<2, LO, false>(a, m, rb, srow_s, st, T, acc);
+    }
     // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + 16 wv + n
     const int row = rb + 16 * wv + (lane & 15), q = lane >> 4;
     if (row >= (int)a.out_dim) return;
@@ -622,11 +648,11 @@ static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
 }
 
 static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
-    const uint32_t rowblocks = (a.out_dim + 63) / 64;
+    const uint32_t rowblocks = (a.out_dim + PF_ROWS - 1) / PF_ROWS;
     const uint32_t nmat = a.mode == 0 ? 2 : 1;
     // whole multiple of 8 blocks (the XCD-aware unit order); extra units exit
     const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
-    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(256);
+    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(PF_NT);
     if (lo)
         hipLaunchKernelGGL(fm_pf_gemm_kernel<true>, grid, block, 0, st, a);
     else
