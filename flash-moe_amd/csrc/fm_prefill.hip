@@ -34,6 +34,7 @@ typedef _Float16 fm_h8 __attribute__((ext_vector_type(8)));
 typedef float fm_f4v __attribute__((ext_vector_type(4)));
 
 #define PF_TOK 16    // token columns per MFMA N tile
+#define PF_CROW 32   // ints per chunk row: expert, entry offset, count, bits, blob address (2), pad, 16 slot ids
 #define PF_CHUNK PF_TOK  // entries per chunk (one block covers a chunk x 64 rows)
 #define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: one fused decode step per token
 #define PF_TS 68     // words per row of a wave's transpose buffer (64 + 4 pad: no bank conflicts)
@@ -59,7 +60,7 @@ struct PfArgs {
     int pbits;
     int mode;  // 0: gate and up -> G, U rows; 1: down -> y rows; 2: plain matrix -> Y rows
     // work lists
-    const int *chunks;  // [max_chunks][4]: expert, entry offset, count, pad
+    const int *chunks;  // [max_chunks][PF_CROW] chunk rows (see fm_pf_lists_kernel)
     const int *nchunks;
     const int *entries;  // entry -> slot id
     int T, K;
@@ -75,7 +76,8 @@ struct PfArgs {
     float *y;            // mode 1: [slots][hidden]; mode 2: [T][out_dim]
 };
 
-__device__ __forceinline__ PfMat pf_mat(const PfArgs &a, int e, int which, int &bits) {
+// blob / cbits: the chunk row's resolved blob address and bit width (pool experts)
+__device__ __forceinline__ PfMat pf_mat(const PfArgs &a, int e, int which, const char *blob, int cbits, int &bits) {
     PfMat m;
     if (a.mode == 2) {
         bits = a.pbits;
@@ -91,8 +93,7 @@ __device__ __forceinline__ PfMat pf_mat(const PfArgs &a, int e, int which, int &
         m.b = a.sh_b[which];
         return m;
     }
-    const char *blob = (const char *)a.blobs[e];
-    bits = a.bits_table[e];
+    bits = cbits;
     const uint64_t *off = bits == 2 ? a.off2 : a.off4;
     m.w = (const uint32_t *)(blob + off[3 * which + 0]);
     m.s = (const uint16_t *)(blob + off[3 * which + 1]);
@@ -299,9 +300,29 @@ __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageReg
     if (t < PF_TOK * PF_GPP) st.xsum[(t >> 4) & 7][t & 15] = r.xs;
 }
 
-template <int BITS, bool LO, bool VEC>
-__device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *srow, PfStage<LO> (&st)[2],
-                         uint32_t *T, fm_f4v &acc) {
+// Row-tile count of a workgroup: when the whole input fits the two token
+// stages (np <= 2 pieces, e.g. the down projection's 1024 inputs) the chunk's
+// operands stay resident in LDS and one workgroup walks PF_RL row blocks, the
+// weight ring running on across them; otherwise one row block per workgroup.
+#ifndef PF_RL
+#define PF_RL 8
+#endif
+#ifndef PF_RING8
+#define PF_RING8 2  // weight ring depth of the eight-stage (gate/up) kernel
+#endif
+#ifndef PF_RL8
+#define PF_RL8 8    // row blocks of a workgroup holding eight stages (gate/up: 512 rows of 1024)
+#endif
+// nst: token stages the workgroup holds (2, or 8 for the one-per-CU gate/up kernel)
+__host__ __device__ inline int pf_row_tiles(uint32_t in_dim, int nst) {
+    return in_dim / 64 <= (uint32_t)nst * PF_GPP ? (nst == 8 ? PF_RL8 : PF_RL) : 1;
+}
+
+// DUAL: the workgroup computes the same rows of two matrices (gate and up)
+// from one token stage, so the chunk's operands stream once for both.
+template <int BITS, bool LO, bool VEC, bool DUAL, int NST, typename Emit>
+__device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, int rb, int rl, const int *srow,
+                         PfStage<LO> (&st)[NST], uint32_t *T, Emit emit) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, kq = lane >> 4;
     const uint32_t G = a.in_dim / 64;
     constexpr int WPG = 2 * BITS;     // words per group
@@ -310,32 +331,31 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *s
     constexpr int RS = BITS == 4 ? 4 : 8;  // rows between a lane's loads
     const uint32_t wpr = G * WPG;
     const int np = (int)((G + PF_GPP - 1) / PF_GPP);
+    const int nq = np * rl;  // (row tile, piece) steps
     const fm_h2 *xop = a.xop[BITS == 4 ? 0 : 1];
     const fm_h2 *xlo = a.xlo[BITS == 4 ? 0 : 1];
-    const int r0 = rb + 16 * wv;
-    acc = (fm_f4v){0.f, 0.f, 0.f, 0.f};
     const int lrow = BITS == 4 ? kq : (lane >> 3);
     const int lw = BITS == 4 ? 4 * n : 4 * (lane & 7);
-    const uint32_t *wrow[NL];
-#pragma unroll
-    for (int j = 0; j < NL; j++) wrow[j] = mat.w + (size_t)min(r0 + RS * j + lrow, (int)a.out_dim - 1) * wpr;
-    const int srow_r = min(r0 + n, (int)a.out_dim - 1);  // this lane's fold row
-    const uint16_t *sp = mat.s + (size_t)srow_r * G, *bp = mat.b + (size_t)srow_r * G;
-    auto load_piece = [&](int p, PfPiece<BITS> &d) {
-        const int pc = min(p, np - 1);  // past the end: re-read the last piece (no branch)
+    const int last_row = (int)a.out_dim - 1;
+    // step q: piece q % np of row tile q / np (past the end: re-read the last step, no branch)
+    auto load_piece = [&](const PfMat &mat, int q, PfPiece<BITS> &d) {
+        const int qc = min(q, nq - 1);
+        const int rt = qc / np, pc = qc - rt * np;
+        const int r0 = rb + PF_ROWS * rt + 16 * wv;
         const uint32_t w = min((uint32_t)(PW * pc + lw), wpr - 4);
 #pragma unroll
-        for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(wrow[j] + w);
+        for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(mat.w + (size_t)min(r0 + RS * j + lrow, last_row) * wpr + w);
+        const size_t so = (size_t)min(r0 + n, last_row) * G;  // this lane's fold row
         const uint32_t g0 = PF_GPP * pc;
         if constexpr (VEC) {  // G % PF_GPP == 0: the piece's 8 scales are one 16-byte run
-            d.s = *(const FM_GLOBAL fm_u4 *)(sp + g0);
-            d.b = *(const FM_GLOBAL fm_u4 *)(bp + g0);
+            d.s = *(const FM_GLOBAL fm_u4 *)(mat.s + so + g0);
+            d.b = *(const FM_GLOBAL fm_u4 *)(mat.b + so + g0);
         } else {
             uint32_t ws_[4] = {0u, 0u, 0u, 0u}, wb_[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int gg = 0; gg < PF_GPP; gg++) {
                 const uint32_t gi = min(g0 + gg, G - 1);
-                const uint32_t vs = fm_ldg_u16(sp + gi), vb = fm_ldg_u16(bp + gi);
+                const uint32_t vs = fm_ldg_u16(mat.s + so + gi), vb = fm_ldg_u16(mat.b + so + gi);
                 ws_[gg >> 1] |= (g0 + gg < G ? vs : 0u) << (16 * (gg & 1));
                 wb_[gg >> 1] |= (g0 + gg < G ? vb : 0u) << (16 * (gg & 1));
             }
@@ -343,135 +363,201 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, int rb, const int *s
             d.b = (fm_u4){wb_[0], wb_[1], wb_[2], wb_[3]};
         }
     };
-    // Ring of PF_RING pieces with static slots: the piece loop is unrolled by
+    // one piece: transpose this wave's 16 rows through LDS, 2 (4 with LO)
+    // MFMAs and one fold per group
+    auto compute = [&](const PfPiece<BITS> &cur, const PfStage<LO> &cs, fm_f4v &acc) {
+#pragma unroll
+        for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
+        const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+#pragma unroll
+        for (int gg = 0; gg < PF_GPP; gg++) {
+            fm_h8 c0, c1;
+            if constexpr (BITS == 4) {
+                const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
+                c0 = pf_codes<4>((uint32_t)w2, 0);
+                c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
+            } else {
+                const uint32_t w = T[n * PF_TS + 4 * gg + kq];
+                c0 = pf_codes<2>(w, 0);
+                c1 = pf_codes<2>(w, 1);
+            }
+            const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
+            const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
+            fm_f4v d = {0.f, 0.f, 0.f, 0.f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, c0, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, c1, d, 0, 0, 0);
+            if constexpr (LO) {
+                const fm_h8 l0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq]);
+                const fm_h8 l1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq + 4]);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, c0, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
+            }
+            const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
+            const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
+            const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
+            if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
+        }
+    };
+    // Ring of PF_RING pieces with static slots: the step loop is unrolled by
     // PF_RING, so no register ever moves between slots (a move would wait for
-    // the slot's loads) and every piece issues the same loads -- the in-order
+    // the slot's loads) and every step issues the same loads -- the in-order
     // wait counts stay exact and PF_RING - 1 pieces stay in flight while one
-    // is computed.  Token stages: piece p + 1's registers are stored to LDS
-    // while piece p + 2's are already loading.
-    constexpr int R = PF_RING;
-    PfPiece<BITS> ring[R];
+    // is computed.
+    constexpr int R = NST == 8 ? PF_RING8 : PF_RING;
+    fm_f4v acc = (fm_f4v){0.f, 0.f, 0.f, 0.f}, acc2 = acc;
+    PfPiece<BITS> ring[R], ring2[DUAL ? R : 1];
+    if (np <= NST) {
+        // resident operands: the stages hold the whole input, loaded once
+        // (before the weights: piece 0 needs them as early as its weights)
+        PfStageRegs<LO> sr[NST];
 #pragma unroll
-    for (int k = 0; k < R; k++) load_piece(k, ring[k]);
-    PfStageRegs<LO> sr[2];
-    pf_stage_load<LO>(a, srow, xop, xlo, 0, sr[0]);
-    pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
-    pf_stage_store<LO>(st[0], sr[0]);
-    __syncthreads();
-    FM_PF_MARK(1);
-    for (int p0 = 0; p0 < np; p0 += R) {
+        for (int k = 0; k < NST; k++)
+            if (k < np) pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)k * PF_GPP, sr[k]);
 #pragma unroll
-        for (int i = 0; i < R; i++) {
-            const int p = p0 + i;
-            if (p < np) {
-                pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 2, np - 1) * PF_GPP, sr[i & 1]);
-                PfStage<LO> &cs = st[i & 1];
-                const PfPiece<BITS> &cur = ring[i];
-                // transpose this wave's 16 rows of the piece through LDS
+        for (int k = 0; k < R; k++) {
+            load_piece(mat, k, ring[k]);
+            if constexpr (DUAL) load_piece(mat2, k, ring2[k]);
+        }
 #pragma unroll
-                for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
-                __builtin_amdgcn_sched_barrier(0);
-                const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
-                const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+        for (int k = 0; k < NST; k++)
+            if (k < np) pf_stage_store<LO>(st[k], sr[k]);
+        __syncthreads();
+        FM_PF_MARK(1);
+        for (int q0 = 0; q0 < nq; q0 += R) {
 #pragma unroll
-                for (int gg = 0; gg < PF_GPP; gg++) {
-                    fm_h8 c0, c1;
-                    if constexpr (BITS == 4) {
-                        const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
-                        c0 = pf_codes<4>((uint32_t)w2, 0);
-                        c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
-                    } else {
-                        const uint32_t w = T[n * PF_TS + 4 * gg + kq];
-                        c0 = pf_codes<2>(w, 0);
-                        c1 = pf_codes<2>(w, 1);
+            for (int i = 0; i < R; i++) {
+                const int q = q0 + i;
+                __builtin_amdgcn_sched_barrier(0);  // keep the unrolled steps apart (registers)
+                if (q < nq) {
+                    const int rt = q / np, pc = q - rt * np;
+                    compute(ring[i], st[pc], acc);
+                    load_piece(mat, q + R, ring[i]);
+                    if constexpr (DUAL) {
+                        compute(ring2[i], st[pc], acc2);
+                        load_piece(mat2, q + R, ring2[i]);
                     }
-                    const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
-                    const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
-                    fm_f4v d = {0.f, 0.f, 0.f, 0.f};
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, c0, d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, c1, d, 0, 0, 0);
-                    if constexpr (LO) {
-                        const fm_h8 l0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq]);
-                        const fm_h8 l1 =
-                            __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[LO ? 1 : 0][n][32 * gg + 8 * kq + 4]);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, c0, d, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
+                    if (pc == np - 1) {
+                        emit(rt, acc, acc2);
+                        acc = (fm_f4v){0.f, 0.f, 0.f, 0.f};
+                        acc2 = acc;
                     }
-                    const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
-                    const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
-                    const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
-                    if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
                 }
-                if (p == 0) FM_PF_MARK(2);
-                load_piece(p + R, ring[i]);
-                if (p + 1 < np) pf_stage_store<LO>(st[(i + 1) & 1], sr[(i + 1) & 1]);
-                __syncthreads();
             }
         }
+    } else {
+      if constexpr (NST == 2) {
+        // streamed operands: piece p + 1's stage registers go to LDS while
+        // piece p + 2's are already loading; one barrier per piece
+        PfStageRegs<LO> sr[2];
+        pf_stage_load<LO>(a, srow, xop, xlo, 0, sr[0]);
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            load_piece(mat, k, ring[k]);
+            if constexpr (DUAL) load_piece(mat2, k, ring2[k]);
+        }
+        pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
+        pf_stage_store<LO>(st[0], sr[0]);
+        __syncthreads();
+        FM_PF_MARK(1);
+        for (int p0 = 0; p0 < np; p0 += R) {
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int p = p0 + i;
+                __builtin_amdgcn_sched_barrier(0);  // keep the unrolled steps apart (registers)
+                if (p < np) {
+                    pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 2, np - 1) * PF_GPP, sr[i & 1]);
+                    compute(ring[i], st[i & 1], acc);
+                    if (p == 0) FM_PF_MARK(2);
+                    load_piece(mat, p + R, ring[i]);
+                    if constexpr (DUAL) {
+                        compute(ring2[i], st[i & 1], acc2);
+                        load_piece(mat2, p + R, ring2[i]);
+                    }
+                    if (p + 1 < np) pf_stage_store<LO>(st[(i + 1) & 1], sr[(i + 1) & 1]);
+                    __syncthreads();
+                }
+            }
+        }
+        emit(0, acc, acc2);
+      }
     }
     FM_PF_MARK(3);
 }
 
-// grid: blockIdx = ((row block * nmat) + matrix) * max_chunks + chunk, so the
+// grid: blockIdx = row block * max_chunks + chunk, so the
 // blocks that read the same weights for consecutive chunks run side by side
-template <bool LO>
-__global__ __launch_bounds__(PF_NT, PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
-    __shared__ PfStage<LO> st[2];
+template <bool LO, bool DUAL, int NST>
+__global__ __launch_bounds__(PF_NT, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
+    __shared__ PfStage<LO> st[NST];
     __shared__ uint32_t tbuf[PF_W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t nmat = a.mode == 0 ? 2 : 1;
     // XCD-aware order: the 8 XCDs take blocks round-robin, so give XCD x a
     // contiguous range of units -- the chunks of one expert (consecutive units)
     // then share that XCD's L2 instead of fetching the weights once per XCD.
     const uint32_t per_xcd = gridDim.x / 8;
     const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    // mode 0 without DUAL: gate and up rows are separate units (matrix = mat)
+    const uint32_t nmat = (a.mode == 0 && !DUAL) ? 2 : 1;
     const uint32_t ci = u % a.max_chunks, rest = u / a.max_chunks;
     const uint32_t mat = rest % nmat, rbk = rest / nmat;
-    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + PF_ROWS - 1) / PF_ROWS) return;
+    const uint32_t rows_per_wg = PF_ROWS * pf_row_tiles(a.in_dim, NST);
+    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + rows_per_wg - 1) / rows_per_wg) return;
     FM_PF_MARK(0);
-    const int *ch = a.chunks + 4 * ci;
-    const int e = ch[0], off = ch[1], n = ch[2];
+    // one 128-byte chunk row holds everything this workgroup needs
+    const int *ch = a.chunks + (size_t)PF_CROW * ci;
+    const int e = ch[0], off = ch[1], n = ch[2], cbits = ch[3];
+    const char *blob = (const char *)(((uint64_t)(uint32_t)ch[5] << 32) | (uint32_t)ch[4]);
     if (threadIdx.x < PF_TOK) {
         const int ei = threadIdx.x;
-        int sl = -1, sr = -1;
-        if (ei < n) {
-            sl = a.entries[off + ei];
-            sr = a.mode == 1 ? off + ei : (a.mode == 2 ? sl : pf_token_of_slot(a, sl));
-        }
+        const int sl = ch[16 + ei];
+        const int sr = sl < 0 ? -1 : (a.mode == 1 ? off + ei : (a.mode == 2 ? sl : pf_token_of_slot(a, sl)));
         slot_s[ei] = sl;
         srow_s[ei] = sr;
     }
     __syncthreads();
     int bits = 4;
-    const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), bits);
-    const int rb = rbk * PF_ROWS;
-    fm_f4v acc;
+    // mode 0: gate (matrix 0) and up (matrix 1) rows together
+    const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), blob, cbits, bits);
+    const PfMat m2 = DUAL ? pf_mat(a, e, 1, blob, cbits, bits) : m;
+    const int rl = pf_row_tiles(a.in_dim, NST);
+    const int rb = rbk * PF_ROWS * rl;
     uint32_t *T = tbuf[wv];
-    const bool vec = (a.in_dim / 64) % PF_GPP == 0;
+    // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + PF_ROWS rt + 16 wv + n
+    auto emit = [&](int rt, const fm_f4v &acc, const fm_f4v &acc2) {
+        const int row = rb + PF_ROWS * rt + 16 * wv + (lane & 15), q = lane >> 4;
+        if (row >= (int)a.out_dim) return;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int tk = 4 * q + v;
+            if (tk >= n) continue;
+            if constexpr (DUAL) {
+                a.gout[(size_t)(off + tk) * a.out_dim + row] = acc[v];
+                a.uout[(size_t)(off + tk) * a.out_dim + row] = acc2[v];
+            } else if (a.mode == 0) {
+                (mat == 0 ? a.gout : a.uout)[(size_t)(off + tk) * a.out_dim + row] = acc[v];
+            } else {
+                a.y[(size_t)slot_s[tk] * a.out_dim + row] = acc[v];
+            }
+        }
+    };
+    // DUAL kernels are only launched when the scales of a piece are one
+    // 16-byte run (in_dim a multiple of 512)
+    const bool vec = DUAL || (a.in_dim / 64) % PF_GPP == 0;
     if (bits == 4) {
         if (vec)
-            pf_block<4, LO, true>(a, m, rb, srow_s, st, T, acc);
-        else
-            pf_block<4, LO, false>(a, m, rb, srow_s, st, T, acc);
+            pf_block<4, LO, true, DUAL, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+        else if constexpr (!DUAL)
+            pf_block<4, LO, false, false, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
     } else {
         if (vec)
-            pf_block<2, LO, true>(a, m, rb, srow_s, st, T, acc);
-        else
-            pf_block<2, LO, false>(a, m, rb, srow_s, st, T, acc);
-    }
-    // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + 16 wv + n
-    const int row = rb + 16 * wv + (lane & 15), q = lane >> 4;
-    if (row >= (int)a.out_dim) return;
-    float *dst = a.mode == 0 ? (mat == 0 ? a.gout : a.uout) : a.y;
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int tk = 4 * q + v;
-        if (tk >= n) continue;
-        const size_t r = a.mode == 0 ? (size_t)(off + tk) : (size_t)slot_s[tk];
-        dst[r * a.out_dim + row] = acc[v];
+            pf_block<2, LO, true, DUAL, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+        else if constexpr (!DUAL)
+            pf_block<2, LO, false, false, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
     }
     FM_PF_MARK(4);
 }
@@ -480,8 +566,13 @@ __global__ __launch_bounds__(PF_NT, PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
 // Single block: count tokens per expert, scan, scatter entries, cut chunks.
 // Entry order inside an expert is irrelevant to the result (each token column
 // is computed independently), so LDS atomics are fine.
+// Chunk row (PF_CROW ints, one 128-byte line): [0] expert, [1] entry offset,
+// [2] entry count, [3] bit width, [4..5] blob address (pool experts), [16..31]
+// the chunk's slot ids (-1 past the count) -- everything a GEMM workgroup
+// needs in ONE dependent load.
 __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T, int K, int E, int has_shared,
-                                                           int *entries, int *chunks, int *nchunks,
+                                                           const void *const *blobs, const uint8_t *bits_table,
+                                                           int sh_bits, int *entries, int *chunks, int *nchunks,
                                                            uint32_t max_chunks, int *err) {
     extern __shared__ int sm[];
     int *cnt = sm;               // [E + 1]
@@ -518,13 +609,19 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     // chunks
     for (int e = threadIdx.x; e < NE; e += blockDim.x) {
         const int ne = cnt[e];
+        if (ne == 0) continue;
+        const uint64_t blob = e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
+        const int bits = e < E ? (int)bits_table[e] : sh_bits;
         for (int j = 0; j * PF_CHUNK < ne; j++) {
             const int ci = cbase[e] + j;
             if (ci >= (int)max_chunks) break;
-            chunks[4 * ci + 0] = e;
-            chunks[4 * ci + 1] = base[e] + j * PF_CHUNK;
-            chunks[4 * ci + 2] = min(PF_CHUNK, ne - j * PF_CHUNK);
-            chunks[4 * ci + 3] = 0;
+            int *row = chunks + (size_t)PF_CROW * ci;
+            row[0] = e;
+            row[1] = base[e] + j * PF_CHUNK;
+            row[2] = min(PF_CHUNK, ne - j * PF_CHUNK);
+            row[3] = bits;
+            row[4] = (int)(uint32_t)blob;
+            row[5] = (int)(uint32_t)(blob >> 32);
         }
     }
     __syncthreads();
@@ -539,6 +636,14 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     }
     if (has_shared)
         for (int t = threadIdx.x; t < T; t += blockDim.x) entries[base[E] + t] = T * K + t;
+    __syncthreads();
+    // slot ids into the chunk rows
+    const int nc = min(cbase[NE], (int)max_chunks);
+    for (int q = threadIdx.x; q < nc * PF_CHUNK; q += blockDim.x) {
+        const int ci = q / PF_CHUNK, ei = q % PF_CHUNK;
+        int *row = chunks + (size_t)PF_CROW * ci;
+        row[16 + ei] = ei < row[2] ? entries[row[1] + ei] : -1;
+    }
 }
 
 // ---------------------------------------------------------------- combine --
@@ -605,7 +710,7 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     L.entries = o;
     o += fm_align_up(nent * 4, 256);
     L.chunks = o;
-    o += fm_align_up((size_t)mc * 16, 256);
+    o += fm_align_up((size_t)mc * PF_CROW * 4, 256);
     L.nchunks = o;
     o += 256;
     L.err = o;
@@ -648,15 +753,24 @@ static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
 }
 
 static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
-    const uint32_t rowblocks = (a.out_dim + PF_ROWS - 1) / PF_ROWS;
-    const uint32_t nmat = a.mode == 0 ? 2 : 1;
+    const uint32_t G = a.in_dim / 64;
+    const uint32_t np = (G + PF_GPP - 1) / PF_GPP;
+    // gate and up rows in one workgroup with the whole input resident (eight
+    // stages, one workgroup per CU) when a piece's scales are one 16-byte run
+    const bool dual = !lo && a.mode == 0 && G % PF_GPP == 0 && np <= 8;
+    const int nst = dual ? 8 : 2;
+    const uint32_t rows_per_wg = PF_ROWS * pf_row_tiles(a.in_dim, nst);
+    const uint32_t rowblocks = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
+    const uint32_t nmat = (a.mode == 0 && !dual) ? 2 : 1;
     // whole multiple of 8 blocks (the XCD-aware unit order); extra units exit
     const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
     dim3 grid((unsigned)((units + 7) / 8 * 8)), block(PF_NT);
     if (lo)
-        hipLaunchKernelGGL(fm_pf_gemm_kernel<true>, grid, block, 0, st, a);
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<true, false, 2>), grid, block, 0, st, a);
+    else if (dual)
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, true, 8>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL(fm_pf_gemm_kernel<false>, grid, block, 0, st, a);
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, false, 2>), grid, block, 0, st, a);
     return fm_check_launch("fm_pf_gemm_kernel");
 }
 
@@ -710,8 +824,8 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     size_t lds = ((size_t)pool->num_experts * 3 + 5) * sizeof(int);
     if (lds > 65536) return fm_fail(FM_ERR_UNSUPPORTED, "%s: too many experts", who);
     hipLaunchKernelGGL(fm_pf_lists_kernel, dim3(1), dim3(1024), lds, st, idx, T, K, (int)pool->num_experts,
-                       has_shared, (int *)(p + L.entries), (int *)(p + L.chunks), (int *)(p + L.nchunks), mc,
-                       (int *)(p + L.err));
+                       has_shared, pool->blobs, pool->bits, shared ? shared_bits : 4, (int *)(p + L.entries),
+                       (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err));
     int rc = fm_check_launch("fm_pf_lists_kernel");
     if (rc) return rc;
     // token operands of X (hidden states are bf16-exact: fp16 hi only)
@@ -782,17 +896,21 @@ __global__ void fm_pfb_lists_kernel(int N, int *entries, int *chunks, int *nchun
     if (i < N) entries[i] = i;
     const int nc = (N + PF_CHUNK - 1) / PF_CHUNK;
     if (i < nc) {
-        chunks[4 * i + 0] = 0;
-        chunks[4 * i + 1] = i * PF_CHUNK;
-        chunks[4 * i + 2] = min(PF_CHUNK, N - i * PF_CHUNK);
-        chunks[4 * i + 3] = 0;
+        int *row = chunks + (size_t)PF_CROW * i;
+        const int n = min(PF_CHUNK, N - i * PF_CHUNK);
+        row[0] = 0;
+        row[1] = i * PF_CHUNK;
+        row[2] = n;
+        row[3] = 0;
+        row[4] = row[5] = 0;
+        for (int ei = 0; ei < PF_CHUNK; ei++) row[16 + ei] = ei < n ? i * PF_CHUNK + ei : -1;
     }
     if (i == 0) *nchunks = nc;
 }
 
 static size_t pfb_head(uint32_t N) {
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    return fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * 16, 256) + 256;
+    return fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256) + 256;
 }
 
 extern "C" size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim) {
@@ -816,7 +934,7 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     int *entries = (int *)p;
     int *chunks = (int *)(p + fm_align_up((size_t)N * 4, 256));
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    int *nchunks = (int *)(p + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * 16, 256));
+    int *nchunks = (int *)(p + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256));
     hipStream_t st = fm_stream(stream);
     const uint32_t nt = (uint32_t)(N > nc ? N : nc);
     hipLaunchKernelGGL(fm_pfb_lists_kernel, dim3((nt + 255) / 256), dim3(256), 0, st, (int)N, entries, chunks, nchunks);
