@@ -66,7 +66,12 @@ def _prefill_case(orc, dev, E, Tn, K, H, I, bits_of, seed, zipf=False, shared_bi
 
 
 @pytest.mark.parametrize("E,Tn,K,H,I,mode", [(16, 40, 4, 1024, 512, "4"), (12, 23, 3, 1024, 512, "tiered"),
-                                             (8, 5, 8, 2048, 256, "2"), (64, 12, 10, HIDDEN, INTER, "4")])
+                                             (8, 5, 8, 2048, 256, "2"), (64, 12, 10, HIDDEN, INTER, "4"),
+                                             # gate/up streamed (20 input groups: not whole 8-group
+                                             # pieces), down resident with per-group scale loads
+                                             (10, 30, 3, 1280, 768, "tiered"),
+                                             # ~75 entries per expert: many 16-entry chunks per expert
+                                             (16, 200, 6, 1024, 512, "4")])
 def test_prefill_moe_vs_oracle(orc, dev, E, Tn, K, H, I, mode):
     say("prefill", E, Tn, K, H, I, mode)
     bits_of = (lambda e: 4) if mode == "4" else (lambda e: 2) if mode == "2" else (lambda e: 4 if e % 3 else 2)
