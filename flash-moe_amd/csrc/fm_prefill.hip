@@ -37,7 +37,7 @@ typedef float fm_f4v __attribute__((ext_vector_type(4)));
 #define PF_CROW 32   // ints per chunk row: expert, entry offset, count, bits, blob address (2), pad, 16 slot ids
 #define PF_CHUNK PF_TOK  // entries per chunk (one block covers a chunk x 64 rows)
 #define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: one fused decode step per token
-#define PF_TS 68     // words per row of a wave's transpose buffer (64 + 4 pad: no bank conflicts)
+#define PF_TS 36     // words per row of a wave's transpose buffer: half a 4-bit piece (32 + 4 pad: no bank conflicts)
 
 // One expert's matrices.
 struct PfMat {
@@ -232,15 +232,11 @@ __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict_
 #define PF_RING 2   // pieces of weights in flight (static ring slots; even)
 #endif
 #define PF_XS (PF_GPP * 32 + 4)  // pairs per token row of the stage (+4: no LDS bank conflicts)
-#ifndef PF_W
-#define PF_W 4      // waves per block: 16 rows each, so a block covers 16 * PF_W rows
-#endif
 #ifndef PF_MINB
-#define PF_MINB 2   // blocks per CU the register budget is sized for
+#define PF_MINB 2   // blocks per CU the register budget of the two-stage kernels is sized for
 #endif
-#define PF_NT (64 * PF_W)
-#define PF_ROWS (16 * PF_W)
-#define PF_KS (PF_TOK * PF_GPP * 8 / PF_NT)  // 16-byte stage pieces per thread and operand array
+// 16-byte stage pieces per thread and operand array, for W waves per workgroup
+#define PF_KS(W) (PF_TOK * PF_GPP * 8 / (64 * (W)))
 #ifndef FM_PF_MARK
 #define FM_PF_MARK(n)
 #endif
@@ -251,9 +247,9 @@ struct PfStage {
     float xsum[PF_GPP][PF_TOK];
 };
 
-template <bool LO>
+template <bool LO, int W>
 struct PfStageRegs {
-    fm_u4 x[(LO ? 2 : 1) * PF_KS];
+    fm_u4 x[(LO ? 2 : 1) * PF_KS(W)];
     float xs;
 };
 
@@ -265,19 +261,20 @@ struct PfPiece {
 
 // Branch-free stage loads (clamped addresses, zero by select) so the compiler
 // keeps every load of the next piece in flight during the current one.
-template <bool LO>
+template <bool LO, int W>
 __device__ __forceinline__ void pf_stage_load(const PfArgs &a, const int *srow, const fm_h2 *xop, const fm_h2 *xlo,
-                                              uint32_t g0, PfStageRegs<LO> &r) {
+                                              uint32_t g0, PfStageRegs<LO, W> &r) {
+    constexpr int KS = PF_KS(W);
     const int t = threadIdx.x;
     const uint32_t G = a.in_dim / 64;
 #pragma unroll
-    for (int k = 0; k < (LO ? 2 : 1) * PF_KS; k++) {
-        const int i = t + PF_NT * (k % PF_KS);
+    for (int k = 0; k < (LO ? 2 : 1) * KS; k++) {
+        const int i = t + 64 * W * (k % KS);
         const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
         const int sr = srow[tok];
         const uint32_t g = g0 + gg;
         const bool ok = sr >= 0 && g < G;
-        const fm_h2 *base = k < PF_KS ? xop : xlo;
+        const fm_h2 *base = k < KS ? xop : xlo;
         const fm_u4 v = *(const FM_GLOBAL fm_u4 *)(base + ((size_t)(ok ? sr : 0) * G + (ok ? g : 0)) * 32 + 4 * part);
         r.x[k] = ok ? v : (fm_u4){0u, 0u, 0u, 0u};
     }
@@ -288,14 +285,15 @@ __device__ __forceinline__ void pf_stage_load(const PfArgs &a, const int *srow, 
     r.xs = ok ? v : 0.f;
 }
 
-template <bool LO>
-__device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageRegs<LO> &r) {
+template <bool LO, int W>
+__device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageRegs<LO, W> &r) {
+    constexpr int KS = PF_KS(W);
     const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < (LO ? 2 : 1) * PF_KS; k++) {
-        const int i = t + PF_NT * (k % PF_KS);
+    for (int k = 0; k < (LO ? 2 : 1) * KS; k++) {
+        const int i = t + 64 * W * (k % KS);
         const int tok = i >> 6, gg = (i >> 3) & 7, part = i & 7;
-        *(fm_u4 *)&st.xop[k / PF_KS][tok][32 * gg + 4 * part] = r.x[k];
+        *(fm_u4 *)&st.xop[k / KS][tok][32 * gg + 4 * part] = r.x[k];
     }
     if (t < PF_TOK * PF_GPP) st.xsum[(t >> 4) & 7][t & 15] = r.xs;
 }
@@ -311,7 +309,7 @@ __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageReg
 #define PF_RING8 2  // weight ring depth of the eight-stage (gate/up) kernel
 #endif
 #ifndef PF_RL8
-#define PF_RL8 8    // row blocks of a workgroup holding eight stages (gate/up: 512 rows of 1024)
+#define PF_RL8 4    // row blocks of a workgroup holding eight stages (8 waves: 512 rows of 1024)
 #endif
 // nst: token stages the workgroup holds (2, or 8 for the one-per-CU gate/up kernel)
 __host__ __device__ inline int pf_row_tiles(uint32_t in_dim, int nst) {
@@ -320,7 +318,7 @@ __host__ __device__ inline int pf_row_tiles(uint32_t in_dim, int nst) {
 
 // DUAL: the workgroup computes the same rows of two matrices (gate and up)
 // from one token stage, so the chunk's operands stream once for both.
-template <int BITS, bool LO, bool VEC, bool DUAL, int NST, typename Emit>
+template <int BITS, bool LO, bool VEC, bool DUAL, int NST, int W, typename Emit>
 __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, int rb, int rl, const int *srow,
                          PfStage<LO> (&st)[NST], uint32_t *T, Emit emit) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, kq = lane >> 4;
@@ -341,7 +339,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
     auto load_piece = [&](const PfMat &mat, int q, PfPiece<BITS> &d) {
         const int qc = min(q, nq - 1);
         const int rt = qc / np, pc = qc - rt * np;
-        const int r0 = rb + PF_ROWS * rt + 16 * wv;
+        const int r0 = rb + 16 * W * rt + 16 * wv;
         const uint32_t w = min((uint32_t)(PW * pc + lw), wpr - 4);
 #pragma unroll
         for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(mat.w + (size_t)min(r0 + RS * j + lrow, last_row) * wpr + w);
@@ -365,17 +363,22 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
     };
     // one piece: transpose this wave's 16 rows through LDS, 2 (4 with LO)
     // MFMAs and one fold per group
+    // (4-bit pieces pass in two halves of four groups: half the LDS per wave)
     auto compute = [&](const PfPiece<BITS> &cur, const PfStage<LO> &cs, fm_f4v &acc) {
-#pragma unroll
-        for (int j = 0; j < NL; j++) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw] = cur.c[j];
-        __builtin_amdgcn_sched_barrier(0);
         const uint32_t sw[4] = {cur.s.x, cur.s.y, cur.s.z, cur.s.w};
         const uint32_t bw[4] = {cur.b.x, cur.b.y, cur.b.z, cur.b.w};
 #pragma unroll
         for (int gg = 0; gg < PF_GPP; gg++) {
+            if (gg == 0 || (BITS == 4 && gg == PF_GPP / 2)) {
+                const int hf = BITS == 4 ? gg / (PF_GPP / 2) : 0;
+#pragma unroll
+                for (int j = 0; j < NL; j++)
+                    if (BITS != 4 || (lw >> 5) == hf) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw - 32 * hf] = cur.c[j];
+                __builtin_amdgcn_sched_barrier(0);
+            }
             fm_h8 c0, c1;
             if constexpr (BITS == 4) {
-                const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * gg + 2 * kq];
+                const uint64_t w2 = *(const uint64_t *)&T[n * PF_TS + 8 * (gg % (PF_GPP / 2)) + 2 * kq];
                 c0 = pf_codes<4>((uint32_t)w2, 0);
                 c1 = pf_codes<4>((uint32_t)(w2 >> 32), 0);
             } else {
@@ -413,10 +416,10 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
     if (np <= NST) {
         // resident operands: the stages hold the whole input, loaded once
         // (before the weights: piece 0 needs them as early as its weights)
-        PfStageRegs<LO> sr[NST];
+        PfStageRegs<LO, W> sr[NST];
 #pragma unroll
         for (int k = 0; k < NST; k++)
-            if (k < np) pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)k * PF_GPP, sr[k]);
+            if (k < np) pf_stage_load<LO, W>(a, srow, xop, xlo, (uint32_t)k * PF_GPP, sr[k]);
 #pragma unroll
         for (int k = 0; k < R; k++) {
             load_piece(mat, k, ring[k]);
@@ -424,7 +427,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
         }
 #pragma unroll
         for (int k = 0; k < NST; k++)
-            if (k < np) pf_stage_store<LO>(st[k], sr[k]);
+            if (k < np) pf_stage_store<LO, W>(st[k], sr[k]);
         __syncthreads();
         FM_PF_MARK(1);
         for (int q0 = 0; q0 < nq; q0 += R) {
@@ -452,15 +455,15 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
       if constexpr (NST == 2) {
         // streamed operands: piece p + 1's stage registers go to LDS while
         // piece p + 2's are already loading; one barrier per piece
-        PfStageRegs<LO> sr[2];
-        pf_stage_load<LO>(a, srow, xop, xlo, 0, sr[0]);
+        PfStageRegs<LO, W> sr[2];
+        pf_stage_load<LO, W>(a, srow, xop, xlo, 0, sr[0]);
 #pragma unroll
         for (int k = 0; k < R; k++) {
             load_piece(mat, k, ring[k]);
             if constexpr (DUAL) load_piece(mat2, k, ring2[k]);
         }
-        pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
-        pf_stage_store<LO>(st[0], sr[0]);
+        pf_stage_load<LO, W>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
+        pf_stage_store<LO, W>(st[0], sr[0]);
         __syncthreads();
         FM_PF_MARK(1);
         for (int p0 = 0; p0 < np; p0 += R) {
@@ -469,7 +472,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
                 const int p = p0 + i;
                 __builtin_amdgcn_sched_barrier(0);  // keep the unrolled steps apart (registers)
                 if (p < np) {
-                    pf_stage_load<LO>(a, srow, xop, xlo, (uint32_t)min(p + 2, np - 1) * PF_GPP, sr[i & 1]);
+                    pf_stage_load<LO, W>(a, srow, xop, xlo, (uint32_t)min(p + 2, np - 1) * PF_GPP, sr[i & 1]);
                     compute(ring[i], st[i & 1], acc);
                     if (p == 0) FM_PF_MARK(2);
                     load_piece(mat, p + R, ring[i]);
@@ -477,7 +480,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
                         compute(ring2[i], st[i & 1], acc2);
                         load_piece(mat2, p + R, ring2[i]);
                     }
-                    if (p + 1 < np) pf_stage_store<LO>(st[(i + 1) & 1], sr[(i + 1) & 1]);
+                    if (p + 1 < np) pf_stage_store<LO, W>(st[(i + 1) & 1], sr[(i + 1) & 1]);
                     __syncthreads();
                 }
             }
@@ -490,10 +493,12 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
 
 // grid: blockIdx = row block * max_chunks + chunk, so the
 // blocks that read the same weights for consecutive chunks run side by side
-template <bool LO, bool DUAL, int NST>
-__global__ __launch_bounds__(PF_NT, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
+// W waves per workgroup (16 rows each): 4 for the two-stage kernels (two
+// workgroups per CU), 8 for the eight-stage gate/up kernel (one per CU).
+template <bool LO, bool DUAL, int NST, int W>
+__global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
     __shared__ PfStage<LO> st[NST];
-    __shared__ uint32_t tbuf[PF_W][16 * PF_TS];
+    __shared__ uint32_t tbuf[W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     // XCD-aware order: the 8 XCDs take blocks round-robin, so give XCD x a
@@ -505,7 +510,7 @@ __global__ __launch_bounds__(PF_NT, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kern
     const uint32_t nmat = (a.mode == 0 && !DUAL) ? 2 : 1;
     const uint32_t ci = u % a.max_chunks, rest = u / a.max_chunks;
     const uint32_t mat = rest % nmat, rbk = rest / nmat;
-    const uint32_t rows_per_wg = PF_ROWS * pf_row_tiles(a.in_dim, NST);
+    const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, NST);
     if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + rows_per_wg - 1) / rows_per_wg) return;
     FM_PF_MARK(0);
     // one 128-byte chunk row holds everything this workgroup needs
@@ -525,11 +530,11 @@ __global__ __launch_bounds__(PF_NT, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kern
     const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), blob, cbits, bits);
     const PfMat m2 = DUAL ? pf_mat(a, e, 1, blob, cbits, bits) : m;
     const int rl = pf_row_tiles(a.in_dim, NST);
-    const int rb = rbk * PF_ROWS * rl;
+    const int rb = rbk * 16 * W * rl;
     uint32_t *T = tbuf[wv];
-    // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + PF_ROWS rt + 16 wv + n
+    // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + 16 W rt + 16 wv + n
     auto emit = [&](int rt, const fm_f4v &acc, const fm_f4v &acc2) {
-        const int row = rb + PF_ROWS * rt + 16 * wv + (lane & 15), q = lane >> 4;
+        const int row = rb + 16 * W * rt + 16 * wv + (lane & 15), q = lane >> 4;
         if (row >= (int)a.out_dim) return;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
@@ -550,14 +555,14 @@ __global__ __launch_bounds__(PF_NT, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kern
     const bool vec = DUAL || (a.in_dim / 64) % PF_GPP == 0;
     if (bits == 4) {
         if (vec)
-            pf_block<4, LO, true, DUAL, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+            pf_block<4, LO, true, DUAL, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
         else if constexpr (!DUAL)
-            pf_block<4, LO, false, false, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+            pf_block<4, LO, false, false, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
     } else {
         if (vec)
-            pf_block<2, LO, true, DUAL, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+            pf_block<2, LO, true, DUAL, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
         else if constexpr (!DUAL)
-            pf_block<2, LO, false, false, NST>(a, m, m2, rb, rl, srow_s, st, T, emit);
+            pf_block<2, LO, false, false, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
     }
     FM_PF_MARK(4);
 }
@@ -759,18 +764,19 @@ static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     // stages, one workgroup per CU) when a piece's scales are one 16-byte run
     const bool dual = !lo && a.mode == 0 && G % PF_GPP == 0 && np <= 8;
     const int nst = dual ? 8 : 2;
-    const uint32_t rows_per_wg = PF_ROWS * pf_row_tiles(a.in_dim, nst);
+    const int W = dual ? 8 : 4;
+    const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, nst);
     const uint32_t rowblocks = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
     const uint32_t nmat = (a.mode == 0 && !dual) ? 2 : 1;
     // whole multiple of 8 blocks (the XCD-aware unit order); extra units exit
     const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
-    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(PF_NT);
+    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(64 * W);
     if (lo)
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<true, false, 2>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<true, false, 2, 4>), grid, block, 0, st, a);
     else if (dual)
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, true, 8>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, true, 8, 8>), grid, block, 0, st, a);
     else
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, false, 2>), grid, block, 0, st, a);
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, false, 2, 4>), grid, block, 0, st, a);
     return fm_check_launch("fm_pf_gemm_kernel");
 }
 
