@@ -583,11 +583,13 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     int *cnt = sm;               // [E + 1]
     int *base = sm + (E + 1);    // [E + 2]
     int *cbase = base + (E + 2); // [E + 2]
+    __shared__ int wsum[2][16];
     const int NE = E + (has_shared ? 1 : 0);
-    for (int i = threadIdx.x; i <= E; i += blockDim.x) cnt[i] = 0;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
     __syncthreads();
     const int n = T * K;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = tid; i < n; i += blockDim.x) {
         int e = idx[i];
         if (e < 0 || e >= E) {
             atomicOr(err, 1);
@@ -595,24 +597,59 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
         }
         atomicAdd(&cnt[e], 1);
     }
-    if (has_shared && threadIdx.x == 0) cnt[E] = T;
+    if (has_shared && tid == 0) cnt[E] = T;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0, cacc = 0;
-        for (int e = 0; e < NE; e++) {
-            base[e] = acc;
-            cbase[e] = cacc;
-            acc += cnt[e];
-            cacc += (cnt[e] + PF_CHUNK - 1) / PF_CHUNK;
+    // exclusive scans of entries and chunks over experts: thread t owns the
+    // run of PER consecutive experts starting at t * PER
+    {
+        const int PER = (NE + 1023) / 1024;
+        int se = 0, sc = 0;
+        for (int k = 0; k < PER; k++) {
+            const int e = tid * PER + k;
+            if (e < NE) {
+                se += cnt[e];
+                sc += (cnt[e] + PF_CHUNK - 1) / PF_CHUNK;
+            }
         }
-        base[NE] = acc;
-        cbase[NE] = cacc;
-        *nchunks = cacc <= (int)max_chunks ? cacc : (int)max_chunks;
-        if (cacc > (int)max_chunks) atomicOr(err, 2);
+        int ie = se, ic = sc;  // inclusive wave scans
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int oe = __shfl_up(ie, d, 64), oc = __shfl_up(ic, d, 64);
+            if (lane >= d) {
+                ie += oe;
+                ic += oc;
+            }
+        }
+        if (lane == 63) {
+            wsum[0][wv] = ie;
+            wsum[1][wv] = ic;
+        }
+        __syncthreads();
+        int pe = 0, pc = 0;
+        for (int w = 0; w < wv; w++) {
+            pe += wsum[0][w];
+            pc += wsum[1][w];
+        }
+        int ae = pe + ie - se, ac = pc + ic - sc;
+        for (int k = 0; k < PER; k++) {
+            const int e = tid * PER + k;
+            if (e < NE) {
+                base[e] = ae;
+                cbase[e] = ac;
+                ae += cnt[e];
+                ac += (cnt[e] + PF_CHUNK - 1) / PF_CHUNK;
+            }
+        }
+        if (tid == 1023) {
+            base[NE] = ae;
+            cbase[NE] = ac;
+            *nchunks = ac <= (int)max_chunks ? ac : (int)max_chunks;
+            if (ac > (int)max_chunks) atomicOr(err, 2);
+        }
     }
     __syncthreads();
-    // chunks
-    for (int e = threadIdx.x; e < NE; e += blockDim.x) {
+    // chunk rows: header and empty slot ids (the scatter fills the live ones)
+    for (int e = tid; e < NE; e += blockDim.x) {
         const int ne = cnt[e];
         if (ne == 0) continue;
         const uint64_t blob = e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
@@ -621,34 +658,35 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             const int ci = cbase[e] + j;
             if (ci >= (int)max_chunks) break;
             int *row = chunks + (size_t)PF_CROW * ci;
+            const int nn = min(PF_CHUNK, ne - j * PF_CHUNK);
             row[0] = e;
             row[1] = base[e] + j * PF_CHUNK;
-            row[2] = min(PF_CHUNK, ne - j * PF_CHUNK);
+            row[2] = nn;
             row[3] = bits;
             row[4] = (int)(uint32_t)blob;
             row[5] = (int)(uint32_t)(blob >> 32);
+            for (int ei = nn; ei < PF_CHUNK; ei++) row[16 + ei] = -1;
         }
     }
+    // scatter entries (slot id t*K + k) into the entry lists and the chunk rows;
+    // cnt becomes a running cursor
     __syncthreads();
-    // scatter entries: reuse cnt as a running cursor
-    for (int i = threadIdx.x; i <= E; i += blockDim.x) cnt[i] = 0;
+    for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = tid; i < n; i += blockDim.x) {
         const int e = idx[i];
         if (e < 0 || e >= E) continue;
         const int p = atomicAdd(&cnt[e], 1);
-        entries[base[e] + p] = i;  // slot id t*K + k
+        entries[base[e] + p] = i;
+        const int ci = cbase[e] + p / PF_CHUNK;
+        if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
     }
     if (has_shared)
-        for (int t = threadIdx.x; t < T; t += blockDim.x) entries[base[E] + t] = T * K + t;
-    __syncthreads();
-    // slot ids into the chunk rows
-    const int nc = min(cbase[NE], (int)max_chunks);
-    for (int q = threadIdx.x; q < nc * PF_CHUNK; q += blockDim.x) {
-        const int ci = q / PF_CHUNK, ei = q % PF_CHUNK;
-        int *row = chunks + (size_t)PF_CROW * ci;
-        row[16 + ei] = ei < row[2] ? entries[row[1] + ei] : -1;
-    }
+        for (int t = tid; t < T; t += blockDim.x) {
+            entries[base[E] + t] = T * K + t;
+            const int ci = cbase[E] + t / PF_CHUNK;
+            if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + t % PF_CHUNK] = T * K + t;
+        }
 }
 
 // ---------------------------------------------------------------- combine --
