@@ -55,6 +55,17 @@ class MoeLayer(ctypes.Structure):
                 ("pool", ExpertPool)]
 
 
+class ExpertExtent(ctypes.Structure):
+    _fields_ = [("offset", ctypes.c_uint64), ("size", ctypes.c_uint64), ("bits", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+class ExpertStoreInfo(ctypes.Structure):
+    _fields_ = [("mode", ctypes.c_int), ("num_layers", ctypes.c_uint32), ("num_experts", ctypes.c_uint32),
+                ("layers_available", ctypes.c_uint32), ("manifest_warnings", ctypes.c_uint32),
+                ("expert_size_4bit", ctypes.c_uint64), ("expert_size_2bit", ctypes.c_uint64)]
+
+
 _lib = None
 
 P = ctypes.c_void_p
@@ -93,6 +104,16 @@ SIGNATURES = {
     "fm_moe_forward_norm": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_moe_prefill_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32, I32]),
     "fm_moe_prefill_forward": (I32, [ctypes.POINTER(MoeLayer), I32, I32, P, P, P, P, P, SZ, P]),
+    "fm_expert_store_open": (I32, [ctypes.c_char_p, I32, U32, U32, U32, U32, U32, I32,
+                                   ctypes.POINTER(P)]),
+    "fm_expert_store_close": (None, [P]),
+    "fm_expert_store_get_info": (I32, [P, ctypes.POINTER(ExpertStoreInfo)]),
+    "fm_expert_get_extent": (I32, [P, I32, I32, ctypes.POINTER(ExpertExtent)]),
+    "fm_expert_layer_bytes": (I32, [P, I32, ctypes.POINTER(ctypes.c_uint64)]),
+    "fm_expert_read": (I32, [P, I32, I32, P, P, P]),
+    "fm_expert_stage_start": (I32, [P, I32, I32, P, P, P]),
+    "fm_expert_stage_wait": (I32, [P, P]),
+    "fm_expert_load_layer": (I32, [P, I32, P, SZ, P, P, ctypes.POINTER(ExpertPool), P]),
 }
 
 
@@ -112,7 +133,8 @@ def lib():
 
 
 def check(rc):
-    if rc != 0:
+    """Raise FmError for a negative status; return non-negative results (counts) unchanged."""
+    if rc < 0:
         raise FmError(rc, lib().fm_last_error().decode())
     return rc
 
@@ -131,3 +153,4 @@ def stream_ptr(stream=None):
 
 
 from .api import *  # noqa: E402,F401,F403
+from .expert_io import *  # noqa: E402,F401,F403
