@@ -41,7 +41,6 @@
 #endif
 #define FM_RT_VPT (FM_RT_MAXE / FM_RT_THREADS)  // logits per thread
 #define FM_RT_SMALL_NCH 16                      // chunks of the one-element-per-thread path
-#define FM_RT_FEW 8                             // survivors of a chunk tested with ballots
 #ifndef FM_RT_MARK
 #define FM_RT_MARK(n)
 #define FM_RT_DECL
@@ -58,14 +57,16 @@ struct FmRouteLds {
     int kth[FM_RT_MAXE / 64];
     int cpre[FM_RT_MAXE / 64];
     float red[2][FM_RT_NW];
-    int M, tie;
+    int M, tie, nsurv;
     int s_id[64];
     float s_val[64];
     // E <= 64 * FM_RT_SMALL_NCH path
     int big[FM_RT_SMALL_NCH][68] __attribute__((aligned(16)));  // chunk values >= its kth bound, -2 padded
     int nbig[FM_RT_SMALL_NCH];
     int c0cnt[64];                                              // chunk 0: #{j < i : p_j >= p_i}
-    int sv[FM_RT_NW][64] __attribute__((aligned(16)));          // per-wavefront survivors in lane order, -2 padded
+    int sv[FM_RT_SMALL_NCH][64] __attribute__((aligned(16)));  // chunk survivors' values in lane order
+    int S_v[FM_RT_SMALL_NCH * 64];                              // all survivors: value bits
+    int S_p[FM_RT_SMALL_NCH * 64];                              // element index * 64 + rank in its chunk's list
 };
 
 FM_DEV float fm_wave_max(float v) {
@@ -190,9 +191,11 @@ __device__ void fm_topk_serial(const int *pb, int E, int K, FmRouteLds &L) {
 // wavefronts, so per-element ballot chains would serialise there):
 //  - chunk 0 has no bound: c_i = #{j < i : p_j >= p_i} is summed over all
 //    wavefronts, wavefront w adding the four j in [4w, 4w+4);
-//  - wavefront c >= 1 tests its survivors p_i > L_c: an earlier element
-//    p_j >= p_i > L_c >= kth[c'] is in big[c'], and an element of the own
-//    chunk p_j >= p_i is itself a survivor, so both counts run over short lists.
+//  - the survivors p_i > L_c of every chunk c >= 1 go into one flat list, and
+//    thread (s, c') counts the elements of chunk c' at or above survivor s: an
+//    earlier element p_j >= p_i > L_c >= kth[c'] is in big[c'], and an element
+//    of the own chunk p_j >= p_i is itself a survivor, so every count runs over
+//    a short list; the 16 counts of a survivor are summed across a DPP row.
 // When U (initial elements plus insertions) fits one wavefront, wavefront 0
 // then ranks U, inverts the ranks and pointer-jumps the eviction chains in
 // registers.  Returns false (uniformly) when U is larger than a wavefront and
@@ -220,83 +223,59 @@ __device__ bool fm_route_small(const int *pb, int pv, int E, int K, int nch, FmR
     const int c = wv;
     const int lc = __builtin_amdgcn_readlane(lb, c & 15);
     if (c >= 1 && c < nch) {
-        const uint64_t own = __ballot(pv > lc);  // padding (-2) never passes; i >= 64 >= K
+        // survivors of chunk c (padding -2 never passes; every i >= 64 >= K): listed in
+        // lane order per chunk, and in one flat list over all chunks
+        const uint64_t own = __ballot(pv > lc);
         const int ns = __builtin_popcountll(own);
-        if (ns > 0 && ns <= FM_RT_FEW) {
-            // few survivors: one ballot per (survivor, earlier chunk), earlier chunks held in registers
-            int q[FM_RT_SMALL_NCH];
-#pragma unroll
-            for (int j = 0; j < FM_RT_SMALL_NCH; j++)
-                if (j < c) q[j] = pb[j * 64 + lane];
-            uint64_t rest = own, insc = 0;
-            while (rest) {
-                int sl[4], v[4], cnt[4];
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    sl[b] = rest ? __builtin_ctzll(rest) : 64;
-                    rest &= rest - 1;  // no-op on 0
-                    const int x = __builtin_amdgcn_readlane(pv, min(sl[b], 63));
-                    v[b] = sl[b] < 64 ? x : 0x7fffffff;
-                    const uint64_t lt = sl[b] < 64 ? (1ull << sl[b]) - 1ull : 0ull;
-                    cnt[b] = __builtin_popcountll(__ballot(pv >= v[b]) & lt);
-                }
-#pragma unroll
-                for (int j = 0; j < FM_RT_SMALL_NCH; j++)
-                    if (j < c) {
-#pragma unroll
-                        for (int b = 0; b < 4; b++) cnt[b] += __builtin_popcountll(__ballot(q[j] >= v[b]));
-                    }
-#pragma unroll
-                for (int b = 0; b < 4; b++)
-                    if (sl[b] < 64 && cnt[b] < K) insc |= 1ull << sl[b];
-            }
-            if (lane == 0) L.ins[c] = insc;  // sole writer of chunk c
-        } else if (ns > 0) {
-            // many survivors: lane-parallel counts over the survivor list and the big[] lists
-            const bool mine = (own >> lane) & 1ull;
-            const int r = fm_mbcnt(own);  // survivors below this lane = list entries before its own
-            L.sv[c][mine ? r : ns + lane - r] = mine ? pv : -2;
-            const int nbv = L.nbig[lane & 15];
-            fm_wave_lds_sync();
-            // below = #{entries e : e < p_i}; an entry counts as p_j >= p_i iff it is not below
-            int below = 0, seen = 0;
-            // own chunk, survivors before lane i (list in lane order)
-            for (int k = 0; k < ns; k += 4) {
-                const int4 e = *reinterpret_cast<const int4 *>(&L.sv[c][k]);
-                below += (k < r ? (int)((unsigned)(e.x - pv) >> 31) : 1) + (k + 1 < r ? (int)((unsigned)(e.y - pv) >> 31) : 1) +
-                         (k + 2 < r ? (int)((unsigned)(e.z - pv) >> 31) : 1) + (k + 3 < r ? (int)((unsigned)(e.w - pv) >> 31) : 1);
-                seen += 4;
-            }
-            // earlier chunks: first 16 entries of each list, next row prefetched
-            int4 cur[4];
-#pragma unroll
-            for (int h = 0; h < 4; h++) cur[h] = *reinterpret_cast<const int4 *>(&L.big[0][4 * h]);
-            for (int cp = 0; cp < c; cp++) {
-                int4 nxt[4];
-                const int cn = min(cp + 1, c - 1);
-#pragma unroll
-                for (int h = 0; h < 4; h++) nxt[h] = *reinterpret_cast<const int4 *>(&L.big[cn][4 * h]);
-#pragma unroll
-                for (int h = 0; h < 4; h++)
-                    below += (int)(((unsigned)(cur[h].x - pv) >> 31) + ((unsigned)(cur[h].y - pv) >> 31) +
-                                   ((unsigned)(cur[h].z - pv) >> 31) + ((unsigned)(cur[h].w - pv) >> 31));
-                seen += 16;
-                const int n = __builtin_amdgcn_readlane(nbv, cp);
-                for (int k = 16; k < n; k += 4) {  // long lists (K > 12 or ties at the bound)
-                    const int4 e = *reinterpret_cast<const int4 *>(&L.big[cp][k]);
-                    below += (int)(((unsigned)(e.x - pv) >> 31) + ((unsigned)(e.y - pv) >> 31) +
-                                   ((unsigned)(e.z - pv) >> 31) + ((unsigned)(e.w - pv) >> 31));
-                    seen += 4;
-                }
-#pragma unroll
-                for (int h = 0; h < 4; h++) cur[h] = nxt[h];
-            }
-            const int cnt = seen - below;
-            const uint64_t insc = __ballot(mine && cnt < K);
-            if (lane == 0) L.ins[c] = insc;  // sole writer of chunk c
+        const bool mine = (own >> lane) & 1ull;
+        const int r = fm_mbcnt(own);
+        int base = 0;
+        if (lane == 0 && ns) base = atomicAdd(&L.nsurv, ns);
+        base = __builtin_amdgcn_readlane(base, 0);
+        if (mine) {
+            L.sv[c][r] = pv;
+            L.S_v[base + r] = pv;
+            L.S_p[base + r] = (c * 64 + lane) * 64 + r;
         }
     }
     FM_RT_MARK(12);
+    __syncthreads();
+    // c_i = #{j < i : p_j >= p_i} for every survivor, thread (s, c') counting the
+    // elements of chunk c' at or above p_s: an earlier chunk's are in its big[] list
+    // (p_j >= p_s > L_c >= kth[c']), the own chunk's are survivors listed before s.
+    // The 16 threads of survivor s are one DPP row; their sum decides the insertion.
+    {
+        const int NS = L.nsurv;
+        const int cp = tid & 15;
+        for (int s0 = 0; s0 < NS; s0 += FM_RT_THREADS / 16) {
+            const int sidx = s0 + (tid >> 4);
+            const bool act = sidx < NS;
+            const int v = act ? L.S_v[sidx] : 0x7fffffff;
+            const int sp = act ? L.S_p[sidx] : 0;
+            const int i = sp >> 6, rs = sp & 63, cs = i >> 6;
+            // the first 16 entries of either list in four loads issued together; entries
+            // past a list's end are -2 (big[]) or masked by index (sv[])
+            const bool own_chunk = act && cp == cs;
+            const int *lst = own_chunk ? &L.sv[cs][0] : &L.big[cp][0];
+            const int n = !act || cp > cs ? 0 : own_chunk ? rs : L.nbig[cp];
+            int cnt = 0;
+            if (n > 0) {
+                int4 e[4];
+#pragma unroll
+                for (int h = 0; h < 4; h++) e[h] = *reinterpret_cast<const int4 *>(lst + 4 * h);
+#pragma unroll
+                for (int h = 0; h < 4; h++)
+                    cnt += (4 * h < n && e[h].x >= v) + (4 * h + 1 < n && e[h].y >= v) +
+                           (4 * h + 2 < n && e[h].z >= v) + (4 * h + 3 < n && e[h].w >= v);
+                for (int k = 16; k < n; k++) cnt += lst[k] >= v;  // long lists (K > 12, ties at the bound)
+            }
+            cnt += fm_row_shr<1>(cnt, 0);
+            cnt += fm_row_shr<2>(cnt, 0);
+            cnt += fm_row_shr<4>(cnt, 0);
+            cnt += fm_row_shr<8>(cnt, 0);
+            if (act && cp == 15 && cnt < K) atomicOr(&L.ins[cs], 1ull << (i & 63));
+        }
+    }
     __syncthreads();
     FM_RT_MARK(7);
     const uint64_t ins0 = __ballot(lane >= K && lane < E && L.c0cnt[lane] < K);
@@ -356,8 +335,11 @@ __device__ bool fm_route_small(const int *pb, int pv, int E, int K, int nch, FmR
             // x_m (position K+m-1) evicts the slot of the element of rank m-1
             int ptr = lane < K ? lane : (valid ? L.tor[lane - K] : lane);
             // chains are shorter than 64: six doublings reach every root
-#pragma unroll
-            for (int round = 0; round < 6; round++) ptr = __builtin_amdgcn_ds_bpermute(ptr << 2, ptr);
+            for (int round = 0; round < 6; round++) {
+                const int nx = __builtin_amdgcn_ds_bpermute(ptr << 2, ptr);
+                if (!__ballot(nx != ptr)) break;  // every chain at its root
+                ptr = nx;
+            }
             FM_RT_MARK(10);
             // the K largest (ranks M .. NU-1) are the final slots
             if (valid && r >= M) {
@@ -399,7 +381,10 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
     if (tid < FM_RT_MAXE / 64) L.ins[tid] = 0ull;
     if (tid < FM_RT_UMAX) L.rank[tid] = 0;
     if (tid < 64) L.c0cnt[tid] = 0;
-    if (tid == 0) L.tie = 0;
+    if (tid == 0) {
+        L.tie = 0;
+        L.nsurv = 0;
+    }
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < FM_RT_NW; w++) mx = fmaxf(mx, L.red[0][w]);
