@@ -491,8 +491,9 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
     FM_PF_MARK(3);
 }
 
-// grid: blockIdx = row block * max_chunks + chunk, so the
-// blocks that read the same weights for consecutive chunks run side by side
+// grid: one block per (chunk, matrix, row block) unit of max_chunks chunks;
+// units are consecutive chunks first, so the blocks that read the same
+// weights for consecutive chunks run side by side
 // W waves per workgroup (16 rows each): 4 for the two-stage kernels (two
 // workgroups per CU), 8 for the eight-stage gate/up kernel (one per CU).
 template <bool LO, bool DUAL, int NST, int W>
@@ -501,17 +502,21 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_ker
     __shared__ uint32_t tbuf[W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    // XCD-aware order: the 8 XCDs take blocks round-robin, so give XCD x a
-    // contiguous range of units -- the chunks of one expert (consecutive units)
-    // then share that XCD's L2 instead of fetching the weights once per XCD.
-    const uint32_t per_xcd = gridDim.x / 8;
-    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    // Units are (chunk, matrix, row block) over the LIVE chunks only (the grid is
+    // sized for max_chunks; surplus blocks exit).  XCD-aware order: the 8 XCDs
+    // take blocks round-robin, so XCD x gets the contiguous eighth x of the
+    // units -- equal work per XCD, and the chunks of one expert (consecutive
+    // units) share that XCD's L2 instead of fetching the weights once per XCD.
     // mode 0 without DUAL: gate and up rows are separate units (matrix = mat)
     const uint32_t nmat = (a.mode == 0 && !DUAL) ? 2 : 1;
-    const uint32_t ci = u % a.max_chunks, rest = u / a.max_chunks;
-    const uint32_t mat = rest % nmat, rbk = rest / nmat;
     const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, NST);
-    if ((int)ci >= *a.nchunks || rbk >= (a.out_dim + rows_per_wg - 1) / rows_per_wg) return;
+    const uint32_t nrb = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
+    const uint32_t nch = (uint32_t)*a.nchunks;
+    const uint32_t live = nch * nmat * nrb, per_xcd = (live + 7) / 8;
+    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (blockIdx.x / 8 >= per_xcd || u >= live) return;
+    const uint32_t ci = u % nch, rest = u / nch;
+    const uint32_t mat = rest % nmat, rbk = rest / nmat;
     FM_PF_MARK(0);
     // one 128-byte chunk row holds everything this workgroup needs
     const int *ch = a.chunks + (size_t)PF_CROW * ci;
