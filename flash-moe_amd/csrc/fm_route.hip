@@ -31,6 +31,7 @@
 // -1e30 (the initial slot value) is represented by -1 and padding by -2.
 #include "fm_device.h"
 #include "fm_internal.h"
+#include "fm_route_dev.h"
 
 #define FM_RT_THREADS 1024
 #define FM_RT_NW (FM_RT_THREADS / 64)
@@ -40,11 +41,6 @@
 #define FM_RT_MAX_PASSES (24 * FM_RT_NW)  // above this the serial replay is cheaper
 #endif
 #define FM_RT_VPT (FM_RT_MAXE / FM_RT_THREADS)  // logits per thread
-#define FM_RT_SMALL_NCH 16                      // chunks of the one-element-per-thread path
-#ifndef FM_RT_MARK
-#define FM_RT_MARK(n)
-#define FM_RT_DECL
-#endif
 
 struct FmRouteLds {
     int U[FM_RT_UMAX];                                     // element index: [0,K) initial, then insertions
@@ -68,288 +64,6 @@ struct FmRouteLds {
     int S_v[FM_RT_SMALL_NCH * 64];                              // all survivors: value bits
     int S_p[FM_RT_SMALL_NCH * 64];                              // element index * 64 + rank in its chunk's list
 };
-
-FM_DEV float fm_wave_max(float v) {
-    v = fmaxf(v, fm_dpp_f<0xB1>(v));
-    v = fmaxf(v, fm_dpp_f<0x4E>(v));
-    v = fmaxf(v, fm_dpp_f<0x124>(v));
-    v = fmaxf(v, fm_dpp_f<0x128>(v));
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
-FM_DEV int fm_wave_max_i(int v) {
-    v = max(v, fm_dpp_i<0xB1>(v));
-    v = max(v, fm_dpp_i<0x4E>(v));
-    v = max(v, fm_dpp_i<0x124>(v));
-    v = max(v, fm_dpp_i<0x128>(v));
-    const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-    const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-    return max(max(r0, r1), max(r2, r3));
-}
-
-FM_DEV int fm_wave_sum_i(int v) {
-    v += fm_dpp_i<0xB1>(v);
-    v += fm_dpp_i<0x4E>(v);
-    v += fm_dpp_i<0x124>(v);
-    v += fm_dpp_i<0x128>(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-           __builtin_amdgcn_readlane(v, 48);
-}
-
-// Inclusive prefix sum across the wavefront.
-FM_DEV int fm_wave_incl_scan(int v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(v, d, 64);
-        if (lane >= d) v += o;
-    }
-    return v;
-}
-
-// Largest value with the low FM_RT_KTH_LOW bits clear that at least K lanes
-// reach: a lower bound of the wave's K-th largest (bitwise radix select over
-// the high bits; the low bits would only tighten the bound slightly).
-#define FM_RT_KTH_LOW 16
-FM_DEV int fm_kth_lower_bound(int x, int K) {
-    int res = 0;
-#pragma unroll
-    for (int b = 30; b >= FM_RT_KTH_LOW; b--) {
-        const int cand = res | (1 << b);
-        if (__builtin_popcountll(__ballot(x >= cand)) >= K) res = cand;
-    }
-    return res;
-}
-
-// Row-local (16-lane) DPP shift right by N; lanes without a source get `fill`.
-template <int N>
-FM_DEV int fm_row_shr(int v, int fill) {
-    return __builtin_amdgcn_update_dpp(fill, v, 0x110 + N, 0xF, 0xF, false);
-}
-
-FM_DEV int fm_mbcnt(uint64_t m) {
-    return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
-}
-
-FM_DEV void fm_wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Serial replay on wavefront 0 (fallback): exact for ties.  The K slot keys
-// are kept sorted across lanes (lane 0 = the minimum, lowest slot first among
-// equal values); an insertion shifts the smaller keys down one lane.
-__device__ void fm_topk_serial(const int *pb, int E, int K, FmRouteLds &L) {
-    const int lane = threadIdx.x;
-    int kval = lane < K ? -1 : 0x7fffffff;
-    int kslot = lane < K ? lane : 64;
-    int kid = 0;
-    int thr = -1;
-    for (int base = 0; base < E; base += 64) {
-        const int i = base + lane;
-        const int p = i < E ? pb[i] : -2;
-        uint64_t cand = __ballot(p > thr);
-        while (cand) {
-            const int j = __builtin_ctzll(cand);
-            cand &= cand - 1;
-            const int pj = __builtin_amdgcn_readlane(p, j);
-            if (pj <= thr) continue;
-            const int vslot = __builtin_amdgcn_readfirstlane(kslot);
-            const bool less = lane >= 1 && lane < K && (kval < pj || (kval == pj && kslot < vslot));
-            const int pos = __builtin_popcountll(__ballot(less));
-            // lane i <- lane i+1 (DPP wave_shl:1)
-            const int nval = fm_dpp_i<0x130>(kval);
-            const int nslot = fm_dpp_i<0x130>(kslot);
-            const int nid = fm_dpp_i<0x130>(kid);
-            if (lane < pos) {
-                kval = nval;
-                kslot = nslot;
-                kid = nid;
-            } else if (lane == pos) {
-                kval = pj;
-                kslot = vslot;
-                kid = base + j;
-            }
-            thr = __builtin_amdgcn_readfirstlane(kval);
-        }
-    }
-    if (lane < K) {
-        L.s_val[kslot] = __int_as_float(kval);
-        L.s_id[kslot] = kid;
-    }
-}
-
-// Top-K slots for E <= 64 * FM_RT_SMALL_NCH, one element per thread
-// (wavefront w holds chunk w in pv), called by the whole workgroup once pb,
-// the per-chunk lower bounds kth[] and the lists big[] are in LDS.  The tests
-// are lane-parallel VALU counts (one CU scalar unit serves all 16
-// wavefronts, so per-element ballot chains would serialise there):
-//  - chunk 0 has no bound: c_i = #{j < i : p_j >= p_i} is summed over all
-//    wavefronts, wavefront w adding the four j in [4w, 4w+4);
-//  - the survivors p_i > L_c of every chunk c >= 1 go into one flat list, and
-//    thread (s, c') counts the elements of chunk c' at or above survivor s: an
-//    earlier element p_j >= p_i > L_c >= kth[c'] is in big[c'], and an element
-//    of the own chunk p_j >= p_i is itself a survivor, so every count runs over
-//    a short list; the 16 counts of a survivor are summed across a DPP row.
-// When U (initial elements plus insertions) fits one wavefront, wavefront 0
-// then ranks U, inverts the ranks and pointer-jumps the eviction chains in
-// registers.  Returns false (uniformly) when U is larger than a wavefront and
-// the general path must finish the job.
-__device__ bool fm_route_small(const int *pb, int pv, int E, int K, int nch, FmRouteLds &L) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wv = tid >> 6;
-    // lane c of lb: L_c = max over c' < c of kth[c'] (-1 for chunk 0)
-    int lb = lane < nch - 1 ? L.kth[lane] : -1;
-    lb = max(lb, fm_row_shr<1>(lb, -1));
-    lb = max(lb, fm_row_shr<2>(lb, -1));
-    lb = max(lb, fm_row_shr<4>(lb, -1));
-    lb = max(lb, fm_row_shr<8>(lb, -1));
-    lb = fm_row_shr<1>(lb, -1);
-    {
-        const int q0 = pb[lane];
-        const int4 pj = *reinterpret_cast<const int4 *>(&pb[4 * wv]);
-        const int j0 = 4 * wv;
-        const int part = (lane > j0 && pj.x >= q0) + (lane > j0 + 1 && pj.y >= q0) + (lane > j0 + 2 && pj.z >= q0) +
-                         (lane > j0 + 3 && pj.w >= q0);
-        if (part) atomicAdd(&L.c0cnt[lane], part);
-    }
-    FM_RT_MARK(11);
-    const int c = wv;
-    const int lc = __builtin_amdgcn_readlane(lb, c & 15);
-    if (c >= 1 && c < nch) {
-        // survivors of chunk c (padding -2 never passes; every i >= 64 >= K): listed in
-        // lane order per chunk, and in one flat list over all chunks
-        const uint64_t own = __ballot(pv > lc);
-        const int ns = __builtin_popcountll(own);
-        const bool mine = (own >> lane) & 1ull;
-        const int r = fm_mbcnt(own);
-        int base = 0;
-        if (lane == 0 && ns) base = atomicAdd(&L.nsurv, ns);
-        base = __builtin_amdgcn_readlane(base, 0);
-        if (mine) {
-            L.sv[c][r] = pv;
-            L.S_v[base + r] = pv;
-            L.S_p[base + r] = (c * 64 + lane) * 64 + r;
-        }
-    }
-    FM_RT_MARK(12);
-    __syncthreads();
-    // c_i = #{j < i : p_j >= p_i} for every survivor, thread (s, c') counting the
-    // elements of chunk c' at or above p_s: an earlier chunk's are in its big[] list
-    // (p_j >= p_s > L_c >= kth[c']), the own chunk's are survivors listed before s.
-    // The 16 threads of survivor s are one DPP row; their sum decides the insertion.
-    {
-        const int NS = L.nsurv;
-        const int cp = tid & 15;
-        for (int s0 = 0; s0 < NS; s0 += FM_RT_THREADS / 16) {
-            const int sidx = s0 + (tid >> 4);
-            const bool act = sidx < NS;
-            const int v = act ? L.S_v[sidx] : 0x7fffffff;
-            const int sp = act ? L.S_p[sidx] : 0;
-            const int i = sp >> 6, rs = sp & 63, cs = i >> 6;
-            // the first 16 entries of either list in four loads issued together; entries
-            // past a list's end are -2 (big[]) or masked by index (sv[])
-            const bool own_chunk = act && cp == cs;
-            const int *lst = own_chunk ? &L.sv[cs][0] : &L.big[cp][0];
-            const int n = !act || cp > cs ? 0 : own_chunk ? rs : L.nbig[cp];
-            int cnt = 0;
-            if (n > 0) {
-                int4 e[4];
-#pragma unroll
-                for (int h = 0; h < 4; h++) e[h] = *reinterpret_cast<const int4 *>(lst + 4 * h);
-#pragma unroll
-                for (int h = 0; h < 4; h++)
-                    cnt += (4 * h < n && e[h].x >= v) + (4 * h + 1 < n && e[h].y >= v) +
-                           (4 * h + 2 < n && e[h].z >= v) + (4 * h + 3 < n && e[h].w >= v);
-                for (int k = 16; k < n; k++) cnt += lst[k] >= v;  // long lists (K > 12, ties at the bound)
-            }
-            cnt += fm_row_shr<1>(cnt, 0);
-            cnt += fm_row_shr<2>(cnt, 0);
-            cnt += fm_row_shr<4>(cnt, 0);
-            cnt += fm_row_shr<8>(cnt, 0);
-            if (act && cp == 15 && cnt < K) atomicOr(&L.ins[cs], 1ull << (i & 63));
-        }
-    }
-    __syncthreads();
-    FM_RT_MARK(7);
-    const uint64_t ins0 = __ballot(lane >= K && lane < E && L.c0cnt[lane] < K);
-    const uint64_t im = lane == 0 ? ins0 : lane < nch ? L.ins[lane] : 0ull;
-    if (tid == 0) L.ins[0] = ins0;  // for the general path (read after its next barrier)
-    const int cnt = __builtin_popcountll(im);
-    int incl = cnt;
-    incl += fm_row_shr<1>(incl, 0);
-    incl += fm_row_shr<2>(incl, 0);
-    incl += fm_row_shr<4>(incl, 0);
-    incl += fm_row_shr<8>(incl, 0);
-    const int M = __builtin_amdgcn_readlane(incl, 15);
-    const int NU = K + M;
-    if (NU > 64) return false;
-    // U in LDS: position u < K holds initial element u, insertions follow in index order
-    // (cross-lane reads stay outside lane-divergent code: an inactive lane's value is undefined there)
-    const int pre = __builtin_amdgcn_readlane(incl - cnt, c & 15);
-    if (c < nch) {
-        const uint64_t mc = ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)(im >> 32), c & 15) << 32) |
-                            (unsigned)__builtin_amdgcn_readlane((int)im, c & 15);
-        if ((mc >> lane) & 1ull) {
-            const int pos = K + pre + fm_mbcnt(mc);
-            L.U[pos] = c * 64 + lane;
-            L.Uv[pos] = pv;
-        }
-    }
-    if (wv == 0) {
-        if (lane < K) {
-            L.U[lane] = lane;
-            L.Uv[lane] = pv;
-        } else if (lane >= NU) {
-            L.Uv[lane] = 0x7fffffff;
-        }
-    }
-    __syncthreads();
-    FM_RT_MARK(3);
-    if (wv == 0) {
-        const bool valid = lane < NU;
-        const int vu = L.Uv[lane];
-        const int uu = L.U[lane];
-        // ascending rank; distinct values give a permutation of 0..NU-1
-        int r = 0;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int4 vw[8];
-#pragma unroll
-            for (int w = 0; w < 8; w++) vw[w] = *reinterpret_cast<const int4 *>(&L.Uv[32 * h + 4 * w]);
-#pragma unroll
-            for (int w = 0; w < 8; w++) r += (vw[w].x < vu) + (vw[w].y < vu) + (vw[w].z < vu) + (vw[w].w < vu);
-        }
-        FM_RT_MARK(9);
-        if (fm_wave_sum_i(valid ? r : 0) != NU * (NU - 1) / 2) {
-            fm_topk_serial(pb, E, K, L);  // equal probabilities inside U
-        } else {
-            if (valid) L.tor[r] = lane;
-            fm_wave_lds_sync();
-            // x_m (position K+m-1) evicts the slot of the element of rank m-1
-            int ptr = lane < K ? lane : (valid ? L.tor[lane - K] : lane);
-            // chains are shorter than 64: six doublings reach every root
-            for (int round = 0; round < 6; round++) {
-                const int nx = __builtin_amdgcn_ds_bpermute(ptr << 2, ptr);
-                if (!__ballot(nx != ptr)) break;  // every chain at its root
-                ptr = nx;
-            }
-            FM_RT_MARK(10);
-            // the K largest (ranks M .. NU-1) are the final slots
-            if (valid && r >= M) {
-                L.s_id[ptr] = uu;
-                L.s_val[ptr] = __int_as_float(vu);
-            }
-        }
-    }
-    return true;
-}
 
 __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__restrict__ logits, int T, int E,
                                                                  int K, int *__restrict__ idx,
@@ -415,23 +129,10 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
     if (nch <= FM_RT_SMALL_NCH) {
         // one element per thread: wavefront w holds chunk w in a register
         const int pv = tid < E ? __float_as_int(v[0] * inv) : -2;
-        if (wv < nch - 1) {
-            // the bound, and the chunk's values at or above it (the only ones a later
-            // survivor, being above the bound, can be compared unfavourably with)
-            const int res = fm_kth_lower_bound(pv, K);
-            const uint64_t bm = __ballot(pv >= res);
-            const int n = __builtin_popcountll(bm);
-            const int below = fm_mbcnt(bm);  // members below this lane; the others pad from n on
-            L.big[wv][((bm >> lane) & 1ull) ? below : n + lane - below] = ((bm >> lane) & 1ull) ? pv : -2;
-            if (lane < 4) L.big[wv][64 + lane] = -2;
-            if (lane == 0) {
-                L.kth[wv] = res;
-                L.nbig[wv] = n;
-            }
-        }
+        fm_route_prep<FM_RT_NW>(&pv, K, nch, L);
         __syncthreads();
         FM_RT_MARK(6);
-        done = fm_route_small(pb, pv, E, K, nch, L);
+        done = fm_route_small<FM_RT_NW>(pb, &pv, E, K, nch, L);
     } else {
         __syncthreads();
         // lower bound of the K-th largest of every full chunk but the last
