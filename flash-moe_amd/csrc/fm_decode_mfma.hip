@@ -46,18 +46,53 @@ typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
 #define FM_DX_MARK(n)
 #endif
 
+#define FMM_TAB 1024  // pools up to this many experts: the blob/bits tables are staged in LDS
+
 struct __attribute__((aligned(16))) FmmLds {
     fm_h2 xq[2][FMM_GH][32];  // x as MFMA operand rows: [4-bit | 2-bit layout][group][32 pairs]
     fm_h2 aq[2][FMM_GI][32];  // the B slot's activations, same layouts
     fm_h2 zero[32];           // zero operand rows (128 B)
     float xsum[FMM_GH];       // per-group sums of x
     float asum[FMM_GI];       // per-group sums of the activations
-    float act[FMM_MAXI];      // staged activations (fp32)
+    union {
+        float act[FMM_MAXI];            // staged activations (fp32)
+        const char *tab[FMM_TAB / 2];   // prologue: pool blob table, first half
+    };
+    const char *tab2[FMM_TAB / 2];      // prologue: pool blob table, second half
+    uint8_t tbits[FMM_TAB];             // prologue: pool bit widths
     float part[4][16][2];     // per-wave partial gate/up sums of the A rows
     float ylast[64];          // this block's rows of the last slot's y
     uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
     FmSlot sd[FM_MAX_SLOTS];
 };
+
+// fm_pool_slot with the blob / bits tables read from their LDS copies.
+FM_DEV FmSlot fm_pool_slot_tab(const FmDecodeArgs &a, int e, float w, const char *const *t1, const char *const *t2,
+                               const uint8_t *tb) {
+    FmSlot s;
+    if (e < 0 || (uint32_t)e >= a.pool_n) {
+        s.valid = 0;
+        s.bits = 4;
+        s.weight = 0.f;
+        return s;
+    }
+    const char *blob = e < FMM_TAB / 2 ? t1[e] : t2[e - FMM_TAB / 2];
+    const int bits = tb[e];
+    const uint64_t *off = bits == 2 ? a.off2 : a.off4;
+    s.gw = (const uint32_t *)(blob + off[0]);
+    s.gs = (const uint16_t *)(blob + off[1]);
+    s.gb = (const uint16_t *)(blob + off[2]);
+    s.uw = (const uint32_t *)(blob + off[3]);
+    s.us = (const uint16_t *)(blob + off[4]);
+    s.ub = (const uint16_t *)(blob + off[5]);
+    s.dw = (const uint32_t *)(blob + off[6]);
+    s.ds = (const uint16_t *)(blob + off[7]);
+    s.db = (const uint16_t *)(blob + off[8]);
+    s.bits = bits;
+    s.weight = w;
+    s.valid = blob != nullptr && (bits == 2 || bits == 4);
+    return s;
+}
 
 // One packed word -> the B operand of one MFMA (8 subnormal fp16 codes).
 // 4-bit: [c0 c4 c1' c5' c2 c6 c3' c7'] (' = field *16); 2-bit: half h of the
@@ -266,22 +301,48 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     const int kA = hasA ? (int)(b / tilesA) : 0;
     const int kB = hasB ? (int)(b / tilesB) : 0;
 
-    if (tid < a.S) L.sd[tid] = fm_get_slot(a, tid);
-    if (tid < 32) L.zero[tid] = fm_as_h2(0u);
-    __syncthreads();
-    const FmSlot sA = L.sd[kA], sB = L.sd[kB];
-    const int ph = a.phases ? a.phases : 3;
-    const bool doA = (ph & 1) && hasA && sA.valid, doB = (ph & 2) && hasB && sB.valid;
-
     FM_DX_MARK(0);
     // x first: thread t holds elements 16*(t%4) .. +15 of group t/4.  Loaded
-    // before the weights, so using it later waits only for these loads.
+    // before the slot lookup and the weights, so its latency overlaps theirs.
     fm_f4 xr[4];
     {
         const float *xp = a.x + 16 * tid;
 #pragma unroll
         for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(xp + 4 * j);
     }
+    // Slots.  A pool of up to FMM_TAB experts has its blob/bits tables staged
+    // in LDS together with idx / weights (independent loads, one round trip)
+    // instead of the dependent chain idx -> table entry.
+    const bool tab = a.pool_mode && a.pool_n <= FMM_TAB;
+    int e_k = 0;
+    float w_k = 0.f;
+    if (tab) {
+        if (tid < a.K) {
+            e_k = a.idx[tid];
+            w_k = a.wdev[tid];
+        }
+        for (uint32_t e = tid; e < a.pool_n; e += 256) {
+            const char *p = (const char *)a.pool_blobs[e];
+            if (e < FMM_TAB / 2)
+                L.tab[e] = p;
+            else
+                L.tab2[e - FMM_TAB / 2] = p;
+            L.tbits[e] = a.pool_bits[e];
+        }
+        __syncthreads();
+        if (tid < a.K) {
+            L.sd[tid] = fm_pool_slot_tab(a, e_k, w_k, L.tab, L.tab2, L.tbits);
+        } else if (tid < a.S) {
+            L.sd[tid] = a.slot[tid];
+        }
+    } else if (tid < a.S) {
+        L.sd[tid] = fm_get_slot(a, tid);
+    }
+    if (tid < 32) L.zero[tid] = fm_as_h2(0u);
+    __syncthreads();
+    const FmSlot sA = L.sd[kA], sB = L.sd[kB];
+    const int ph = a.phases ? a.phases : 3;
+    const bool doA = (ph & 1) && hasA && sA.valid, doB = (ph & 2) && hasB && sB.valid;
     // ---- issue every weight load of this wave ----
     const uint32_t rowA0 = (b % tilesA) * 16;
     FmmCodes cg, cu, cdn;
