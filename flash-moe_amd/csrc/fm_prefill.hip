@@ -65,6 +65,7 @@ struct PfArgs {
     const int *entries;  // entry -> slot id
     int T, K;
     uint32_t max_chunks;
+    uint32_t xcd_slots;  // workgroups one XCD runs at once (eight-stage kernel: its CUs)
     // B operands: per source row and group, 32 fp16 pairs in the 4-bit [0] and
     // 2-bit [1] pair layouts (lo: residual terms, mode 2 only) + group sums.
     // Source row: mode 0 token, mode 1 entry position, mode 2 token.
@@ -509,12 +510,30 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_ker
     // units) share that XCD's L2 instead of fetching the weights once per XCD.
     // mode 0 without DUAL: gate and up rows are separate units (matrix = mat)
     const uint32_t nmat = (a.mode == 0 && !DUAL) ? 2 : 1;
-    const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, NST);
+    const int rl_big = pf_row_tiles(a.in_dim, NST);
+    const uint32_t rows_per_wg = 16 * W * rl_big;
     const uint32_t nrb = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
     const uint32_t nch = (uint32_t)*a.nchunks;
     const uint32_t live = nch * nmat * nrb, per_xcd = (live + 7) / 8;
-    const uint32_t u = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (blockIdx.x / 8 >= per_xcd || u >= live) return;
+    // Eight-stage kernel (one workgroup per CU, long units): the units of an
+    // XCD's last partial round run as single row tiles, so that round ends
+    // after about one row tile instead of one whole unit (the grid has room
+    // for the extra workgroups; the others exit).
+    const uint32_t full = (NST == 8 && rl_big > 1) ? per_xcd / a.xcd_slots * a.xcd_slots : per_xcd;
+    const uint32_t nsplit = (per_xcd - full) * (uint32_t)rl_big;
+    const uint32_t lb = blockIdx.x / 8;
+    uint32_t u, tile0 = 0;
+    int rl = rl_big;
+    if (lb < full) {
+        u = (blockIdx.x % 8) * per_xcd + lb;
+    } else if (lb < full + nsplit) {
+        u = (blockIdx.x % 8) * per_xcd + full + (lb - full) / rl_big;
+        tile0 = (lb - full) % rl_big;
+        rl = 1;
+    } else {
+        return;
+    }
+    if (u >= live) return;
     const uint32_t ci = u % nch, rest = u / nch;
     const uint32_t mat = rest % nmat, rbk = rest / nmat;
     FM_PF_MARK(0);
@@ -534,8 +553,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_ker
     // mode 0: gate (matrix 0) and up (matrix 1) rows together
     const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), blob, cbits, bits);
     const PfMat m2 = DUAL ? pf_mat(a, e, 1, blob, cbits, bits) : m;
-    const int rl = pf_row_tiles(a.in_dim, NST);
-    const int rb = rbk * 16 * W * rl;
+    const int rb = (int)(rbk * rows_per_wg + tile0 * 16 * W);
     uint32_t *T = tbuf[wv];
     // lane (row n, q) holds tokens 4q .. 4q+3 of row rb + 16 W rt + 16 wv + n
     auto emit = [&](int rt, const fm_f4v &acc, const fm_f4v &acc2) {
@@ -811,9 +829,12 @@ static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, nst);
     const uint32_t rowblocks = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
     const uint32_t nmat = (a.mode == 0 && !dual) ? 2 : 1;
-    // whole multiple of 8 blocks (the XCD-aware unit order); extra units exit
+    // whole multiple of 8 blocks (the XCD-aware unit order), room for the
+    // eight-stage kernel's split last round; extra blocks exit
     const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
-    dim3 grid((unsigned)((units + 7) / 8 * 8)), block(64 * W);
+    a.xcd_slots = (uint32_t)((fm_num_cus() + 7) / 8);
+    const size_t per_xcd = (units + 7) / 8 + (dual ? (size_t)a.xcd_slots * (pf_row_tiles(a.in_dim, 8) - 1) : 0);
+    dim3 grid((unsigned)(per_xcd * 8)), block(64 * W);
     if (lo)
         hipLaunchKernelGGL((fm_pf_gemm_kernel<true, false, 2, 4>), grid, block, 0, st, a);
     else if (dual)
