@@ -234,7 +234,8 @@ __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict_
 #endif
 #define PF_XS (PF_GPP * 32 + 4)  // pairs per token row of the stage (+4: no LDS bank conflicts)
 #ifndef PF_MINB
-#define PF_MINB 2   // blocks per CU the register budget of the two-stage kernels is sized for
+#define PF_MINB 3   // blocks per CU the register budget of the two-stage kernels is sized for (3 beats 2
+                    // for the down GEMM despite register spills: more loads in flight per CU)
 #endif
 // 16-byte stage pieces per thread and operand array, for W waves per workgroup
 #define PF_KS(W) (PF_TOK * PF_GPP * 8 / (64 * (W)))
