@@ -320,7 +320,8 @@ __host__ __device__ inline int pf_row_tiles(uint32_t in_dim, int nst) {
 
 // DUAL: the workgroup computes the same rows of two matrices (gate and up)
 // from one token stage, so the chunk's operands stream once for both.
-template <int BITS, bool LO, bool VEC, bool DUAL, int NST, int W, typename Emit>
+// RES: the whole input fits the stages (operands resident); else streamed.
+template <int BITS, bool LO, bool VEC, bool DUAL, int NST, int W, bool RES, typename Emit>
 __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, int rb, int rl, const int *srow,
                          PfStage<LO> (&st)[NST], uint32_t *T, Emit emit) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 15, kq = lane >> 4;
@@ -415,7 +416,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
     constexpr int R = NST == 8 ? PF_RING8 : PF_RING;
     fm_f4v acc = (fm_f4v){0.f, 0.f, 0.f, 0.f}, acc2 = acc;
     PfPiece<BITS> ring[R], ring2[DUAL ? R : 1];
-    if (np <= NST) {
+    if constexpr (RES) {
         // resident operands: the stages hold the whole input, loaded once
         // (before the weights: piece 0 needs them as early as its weights)
         PfStageRegs<LO, W> sr[NST];
@@ -498,7 +499,9 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
 // weights for consecutive chunks run side by side
 // W waves per workgroup (16 rows each): 4 for the two-stage kernels (two
 // workgroups per CU), 8 for the eight-stage gate/up kernel (one per CU).
-template <bool LO, bool DUAL, int NST, int W>
+// RES / VEC select one operand path and one scale-load path at compile time,
+// so the registers are sized for the path the launch takes.
+template <bool LO, bool DUAL, int NST, int W, bool RES, bool VEC>
 __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
     __shared__ PfStage<LO> st[NST];
     __shared__ uint32_t tbuf[W][16 * PF_TS];
@@ -574,20 +577,12 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_ker
             }
         }
     };
-    // DUAL kernels are only launched when the scales of a piece are one
-    // 16-byte run (in_dim a multiple of 512)
-    const bool vec = DUAL || (a.in_dim / 64) % PF_GPP == 0;
-    if (bits == 4) {
-        if (vec)
-            pf_block<4, LO, true, DUAL, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
-        else if constexpr (!DUAL)
-            pf_block<4, LO, false, false, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
-    } else {
-        if (vec)
-            pf_block<2, LO, true, DUAL, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
-        else if constexpr (!DUAL)
-            pf_block<2, LO, false, false, NST, W>(a, m, m2, rb, rl, srow_s, st, T, emit);
-    }
+    // VEC: the scales of a piece are one 16-byte run (in_dim a multiple of 512;
+    // DUAL kernels are only launched then)
+    if (bits == 4)
+        pf_block<4, LO, VEC, DUAL, NST, W, RES>(a, m, m2, rb, rl, srow_s, st, T, emit);
+    else
+        pf_block<2, LO, VEC, DUAL, NST, W, RES>(a, m, m2, rb, rl, srow_s, st, T, emit);
     FM_PF_MARK(4);
 }
 
@@ -836,12 +831,22 @@ static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     a.xcd_slots = (uint32_t)((fm_num_cus() + 7) / 8);
     const size_t per_xcd = (units + 7) / 8 + (dual ? (size_t)a.xcd_slots * (pf_row_tiles(a.in_dim, 8) - 1) : 0);
     dim3 grid((unsigned)(per_xcd * 8)), block(64 * W);
-    if (lo)
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<true, false, 2, 4>), grid, block, 0, st, a);
-    else if (dual)
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, true, 8, 8>), grid, block, 0, st, a);
-    else
-        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, false, 2, 4>), grid, block, 0, st, a);
+    const bool res = np <= 2, vec = G % PF_GPP == 0;  // two-stage kernels: resident / vector-scale paths
+#define PF_GO(LO_, R_, V_) hipLaunchKernelGGL((fm_pf_gemm_kernel<LO_, false, 2, 4, R_, V_>), grid, block, 0, st, a)
+#define PF_GO4(LO_)                      \
+    if (res && vec) PF_GO(LO_, true, true);  \
+    else if (res) PF_GO(LO_, true, false);   \
+    else if (vec) PF_GO(LO_, false, true);   \
+    else PF_GO(LO_, false, false);
+    if (lo) {
+        PF_GO4(true)
+    } else if (dual) {
+        hipLaunchKernelGGL((fm_pf_gemm_kernel<false, true, 8, 8, true, true>), grid, block, 0, st, a);
+    } else {
+        PF_GO4(false)
+    }
+#undef PF_GO4
+#undef PF_GO
     return fm_check_launch("fm_pf_gemm_kernel");
 }
 
