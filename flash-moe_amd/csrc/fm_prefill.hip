@@ -567,9 +567,8 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_ker
         for (int v = 0; v < 4; v++) {
             const int tk = 4 * q + v;
             if (tk >= n) continue;
-            if constexpr (DUAL) {
-                a.gout[(size_t)(off + tk) * a.out_dim + row] = acc[v];
-                a.uout[(size_t)(off + tk) * a.out_dim + row] = acc2[v];
+            if constexpr (DUAL) {  // SwiGLU in the epilogue: gout receives the activation
+                a.gout[(size_t)(off + tk) * a.out_dim + row] = fm_silu_mul(acc[v], acc2[v]);
             } else if (a.mode == 0) {
                 (mat == 0 ? a.gout : a.uout)[(size_t)(off + tk) * a.out_dim + row] = acc[v];
             } else {
@@ -814,12 +813,18 @@ static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
     a.xsum = (const float *)(base + P.sum);
 }
 
+// Gate and up rows in one workgroup with the whole input resident (eight
+// stages, one workgroup per CU) when a piece's scales are one 16-byte run; that
+// kernel applies SwiGLU itself (gout receives the activations, uout unused).
+static bool pf_dual(uint32_t in_dim) {
+    const uint32_t G = in_dim / 64;
+    return G % PF_GPP == 0 && (G + PF_GPP - 1) / PF_GPP <= 8;
+}
+
 static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     const uint32_t G = a.in_dim / 64;
     const uint32_t np = (G + PF_GPP - 1) / PF_GPP;
-    // gate and up rows in one workgroup with the whole input resident (eight
-    // stages, one workgroup per CU) when a piece's scales are one 16-byte run
-    const bool dual = !lo && a.mode == 0 && G % PF_GPP == 0 && np <= 8;
+    const bool dual = !lo && a.mode == 0 && pf_dual(a.in_dim);
     const int nst = dual ? 8 : 2;
     const int W = dual ? 8 : 4;
     const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, nst);
@@ -948,7 +953,8 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     rc = pf_launch_gemm(a, false, st);
     if (rc) return rc;
     // act = silu(G) * U as fp16 token operands, then gemm2 (down projection)
-    rc = pf_launch_ops(gout, uout, nullptr, (int)nent, pool->inter, p, L.ao, false, st);
+    rc = pf_launch_ops(gout, pf_dual(pool->hidden) ? nullptr : uout, nullptr, (int)nent, pool->inter, p, L.ao, false,
+                       st);
     if (rc) return rc;
     a.mode = 1;
     pf_bind_ops(a, p, L.ao, false);
