@@ -666,21 +666,27 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
         }
     }
     __syncthreads();
-    // chunk rows: header and empty slot ids (the scatter fills the live ones)
-    for (int e = tid; e < NE; e += blockDim.x) {
-        const int ne = cnt[e];
-        if (ne == 0) continue;
-        const uint64_t blob = e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
-        const int bits = e < E ? (int)bits_table[e] : sh_bits;
-        for (int j = 0; j * PF_CHUNK < ne; j++) {
-            const int ci = cbase[e] + j;
-            if (ci >= (int)max_chunks) break;
+    // chunk rows: header and empty slot ids (the scatter fills the live ones),
+    // one thread per chunk; its expert is the last e with cbase[e] <= chunk
+    {
+        const int nc = min(cbase[NE], (int)max_chunks);
+        for (int ci = tid; ci < nc; ci += blockDim.x) {
+            int lo = 0, hi = NE;  // cbase[lo] <= ci < cbase[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (cbase[mid] <= ci)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
+            const int e = lo, j = ci - cbase[e], ne = cnt[e];
+            const uint64_t blob = e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
             int *row = chunks + (size_t)PF_CROW * ci;
             const int nn = min(PF_CHUNK, ne - j * PF_CHUNK);
             row[0] = e;
             row[1] = base[e] + j * PF_CHUNK;
             row[2] = nn;
-            row[3] = bits;
+            row[3] = e < E ? (int)bits_table[e] : sh_bits;
             row[4] = (int)(uint32_t)blob;
             row[5] = (int)(uint32_t)(blob >> 32);
             for (int ei = nn; ei < PF_CHUNK; ei++) row[16 + ei] = -1;
