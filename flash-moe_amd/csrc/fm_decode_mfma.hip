@@ -27,6 +27,8 @@
 //     The block waits for its slot's I tagged activations, then streams.
 //  C  the blocks of the last slot also combine their 64 rows over all slots
 //     in the slot order of cpu_vec_madd (layer_forward.h:1257, 1295-1305).
+// Hand-off polls re-issue their loads back to back (no sleep between rounds:
+// each round is a memory round trip; sleeping only added latency).
 // Every wave issues all of its gate/up loads before computing, so that stream
 // is in flight from the first microsecond; down-projection loads follow once
 // the wave's own gate/up work is done.
@@ -435,7 +437,6 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
 #pragma unroll
             for (int j = 0; j < MAXQ; j++) ready &= (uint32_t)(t[j] >> 32) == a.epoch;
             if (__all(ready)) break;
-            __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int j = 0; j < MAXQ; j++) {
                 const uint32_t i = j * 256 + tid;
@@ -505,7 +506,6 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
 #pragma unroll
                 for (int k = 0; k < FM_MAX_SLOTS - 1; k++) ready &= (uint32_t)(t[k] >> 32) == a.epoch;
                 if (__all(ready)) break;
-                __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
                     if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)k * H + row]);
@@ -535,7 +535,6 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
                 uint64_t v = lane < (int)tilesB ? fm_get_tagged(&a.ss2[lane]) : ((uint64_t)a.epoch << 32);
                 uint32_t it = 0;
                 while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
-                    __builtin_amdgcn_s_sleep(1);
                     if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.ss2[lane]);
                 }
                 if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
