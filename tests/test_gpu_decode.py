@@ -309,3 +309,37 @@ def test_moe_decode_repeated_calls_one_workspace(orc, dev):
         ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, shared_blob=blobs[K], shared_bits=bl[K],
                              shared_score=score, h_mid=hm)
         assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, rep
+
+
+def _cycled_pool(dev, E, blobs, bits):
+    """A pool of E experts whose blob table cycles over the given device pool's blobs."""
+    import torch
+    n = len(blobs)
+    dp = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    dp.blob_table = torch.from_numpy(np.array([dp.addrs[e % n] for e in range(E)], np.int64)).to(dev)
+    dp.bits_table = torch.from_numpy(np.array([bits[e % n] for e in range(E)], np.uint8)).to(dev)
+    dp.c = fm.ExpertPool(dp.blob_table.data_ptr(), dp.bits_table.data_ptr(), E, HIDDEN, INTER, 64)
+    return dp
+
+
+def test_moe_decode_pool_large_expert_count(orc, dev):
+    """2048 experts: past the LDS-staged pool tables (1024), the slot lookup reads the
+    device tables directly."""
+    import torch
+    say("moe_decode_pool E=2048")
+    bits = [4, 2, 4, 4, 2, 4, 2, 4]
+    blobs = experts(range(3500, 3508), bits)
+    pool = _cycled_pool(dev, 2048, blobs, bits)
+    K = 10
+    rng = synth.rng_for(41)
+    lg = rng.normal(0, 1, (1, 2048)).astype(np.float32)
+    ri, rw = orc.route(lg, K)
+    x = synth.hidden_vec(rng, HIDDEN)
+    hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_decode_pool(pool, T(ri[0].astype(np.int32), dev), T(rw[0], dev), T(x, dev), out, ws, h_mid=T(hm, dev))
+    torch.cuda.synchronize()
+    ref = orc.moe_decode([blobs[e % 8] for e in ri[0]], [bits[e % 8] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                         h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32

@@ -137,3 +137,26 @@ def test_moe_prefill_forward_layer(orc, dev):
     ref = orc.prefill_moe(idx, w, blobs, bits, X, H, I, shared_blob=shared_blob, shared_bits=4,
                           shared_scores=scores, h_mid=hm)
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+def test_prefill_large_expert_count(orc, dev):
+    """2048 experts (blob table cycling over 8 blobs) through the grouped GEMM path."""
+    import torch
+    say("prefill E=2048")
+    E, Tn, K = 2048, 40, 6
+    bits8 = [4, 2, 4, 4, 2, 4, 2, 4]
+    blobs8 = experts(range(3600, 3608), bits8)
+    dp = fm.DevicePool(blobs8, bits8, HIDDEN, INTER)
+    dp.blob_table = T(np.array([dp.addrs[e % 8] for e in range(E)], np.int64), dev)
+    dp.bits_table = T(np.array([bits8[e % 8] for e in range(E)], np.uint8), dev)
+    dp.c = fm.ExpertPool(dp.blob_table.data_ptr(), dp.bits_table.data_ptr(), E, HIDDEN, INTER, 64)
+    rng = synth.rng_for(42)
+    idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
+    X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
+    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, dp), dtype=torch.uint8, device=dev)
+    out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
+    fm.prefill_moe(dp, T(idx, dev), T(w, dev), T(X, dev), out, ws)
+    torch.cuda.synchronize()
+    ref = orc.prefill_moe(idx, w, [blobs8[e % 8] for e in range(E)], [bits8[e % 8] for e in range(E)], X, HIDDEN,
+                          INTER)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
