@@ -122,6 +122,33 @@ def bench_decode(args, dev):
     k1.record()
     torch.cuda.synchronize()
     norm_ms = k0.elapsed_time(k1) / args.steps
+    # the whole MoE block of one decode token through the C layer driver
+    # (fm_moe_forward): router + shared-gate matvecs, routing, fused experts
+    Wr, sr, br = synth.quant_matrix(synth.rng_for(3010), E, H, 4)
+    Wg, sgt, bgt = synth.quant_matrix(synth.rng_for(3011), 1, H, 4)
+    dl = [torch.from_numpy(np.ascontiguousarray(t)).to(dev) for t in (Wr, sr, br, Wg, sgt, bgt)]
+    Lr = fm.MoeLayer()
+    Lr.router_w, Lr.router_s, Lr.router_b = dl[0].data_ptr(), dl[1].data_ptr(), dl[2].data_ptr()
+    Lr.router_bits = 4
+    Lr.seg_w, Lr.seg_s, Lr.seg_b = dl[3].data_ptr(), dl[4].data_ptr(), dl[5].data_ptr()
+    Lr.seg_bits = 4
+    Lr.shared_bits = 4
+    Lr.has_shared = 1
+    Lr.pool = pool.c
+    lws = torch.zeros(fm.moe_forward_workspace_bytes(Lr, K), dtype=torch.uint8, device=dev)
+    hps = torch.from_numpy(synth.hidden_vec(rng, H, (16, H))).to(dev)
+    for i in range(args.warmup):
+        Lr.shared = shared[i % n_sh]
+        fm.moe_forward(Lr, K, hps[i % 16], hm, out, lws, out_bf16=ob)
+    torch.cuda.synchronize()
+    k0.record()
+    for i in range(args.steps):
+        Lr.shared = shared[i % n_sh]
+        fm.moe_forward(Lr, K, hps[i % 16], hm, out, lws, out_bf16=ob)
+    k1.record()
+    torch.cuda.synchronize()
+    layer_ms = k0.elapsed_time(k1) / args.steps
+    router_bytes = E * H // 2 + E * (H // 64) * 4 + H // 2 + (H // 64) * 4
     kern_bytes = (K + 1) * blob + H * 4 * 3 + H * 2
     # unique experts actually touched per step (routing may repeat across steps, never within)
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
@@ -133,6 +160,9 @@ def bench_decode(args, dev):
                      "kernel": "fm_decode_mfma_kernel (one fm_moe_decode_pool call)",
                      "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes,
                      "kernel_us_with_fused_rms_norm": norm_ms * 1e3},
+        "layer_step": {"path": "fm_moe_forward: router + shared-gate matvecs (4-bit) -> routing -> fused experts",
+                       "us": round(layer_ms * 1e3, 2), "bytes": kern_bytes + router_bytes,
+                       "gbs": round((kern_bytes + router_bytes) / (layer_ms * 1e-3) / 1e9, 1)},
     }
     return res, sample_blobs
 
@@ -389,7 +419,8 @@ def main():
         return
     dec, sample = bench_decode(args, dev)
     log(f"decode: {dec['step_ms'] * 1e3:.2f} us/step, {dec['value']:.0f} GB/s; fused launch "
-        f"{dec['roofline']['kernel_us']:.2f} us = {dec['roofline']['achieved']:.0f} GB/s")
+        f"{dec['roofline']['kernel_us']:.2f} us = {dec['roofline']['achieved']:.0f} GB/s; whole MoE block "
+        f"(router + routing + experts) {dec['layer_step']['us']} us")
     pre = None if args.no_prefill else bench_prefill(args, dev, args._pool)
     if pre:
         log(f"prefill: {pre['ms']:.3f} ms/layer, {pre['tokens_per_s']:.0f} tok/s, {pre['hbm_gbs']:.0f} GB/s, "
@@ -413,6 +444,7 @@ def main():
                                "4096->1024->4096 SwiGLU, 4-bit g64, device routing",
                    "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"]},
         "roofline": dec["roofline"],
+        "layer_step": dec["layer_step"],
         "prefill": None if pre is None else {
             "workload": "config 3: 512 tokens, 512 experts, top-10 Zipf(1.1) + shared, grouped MFMA dequant-GEMM",
             "tokens_per_s": round(pre["tokens_per_s"]), "ms_per_layer": pre["ms"],
