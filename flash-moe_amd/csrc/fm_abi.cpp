@@ -95,3 +95,17 @@ int fm_num_cus(void) {
     }
     return cache[dev];
 }
+
+extern "C" int fm_workspace_status(void *ws, uint32_t *status, void *stream) {
+    fm_clear_error();
+    FM_REQUIRE(ws && status, "fm_workspace_status: NULL argument");
+    hipStream_t st = fm_stream(stream);
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyAsync(&v, ws, sizeof v, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = hipMemsetAsync(ws, 0, sizeof v, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return fm_fail(FM_ERR_HIP, "fm_workspace_status: %s", hipGetErrorString(e));
+    *status = v;
+    return FM_OK;
+}

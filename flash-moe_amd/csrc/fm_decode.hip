@@ -149,7 +149,7 @@ __device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmS
             __builtin_amdgcn_s_sleep(1);
             if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(act + i);
         }
-        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
         if (i < a.inter) wbuf[i] = __uint_as_float((uint32_t)v);
     }
     __builtin_amdgcn_wave_barrier();
@@ -208,7 +208,7 @@ __device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, const FmS
             __builtin_amdgcn_s_sleep(1);
             if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]);
         }
-        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
         if (q < n) stage[q] = need ? __uint_as_float((uint32_t)v) : 0.f;
     }
     __builtin_amdgcn_wave_barrier();
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                 if ((uint32_t)(t[q] >> 32) != a.epoch) t[q] = fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i);
             }
         } while (++it < FM_SPIN_MAX);
-        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
 #pragma unroll
         for (int q = 0; q < MAXQ; q++) {
             const uint32_t i = q * 256 + threadIdx.x;
@@ -601,7 +601,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                     }
                 }
             } while (++it < FM_SPIN_MAX);
-            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
             // stage[ui][k][r] holds every slot's y for unit ui (slot kl written above)
             const int i_of_lb = lb - v0;
 #pragma unroll

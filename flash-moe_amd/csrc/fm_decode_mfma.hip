@@ -318,6 +318,10 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     const bool tab = a.pool_mode && a.pool_n <= FMM_TAB;
     int e_k = 0;
     float w_k = 0.f;
+    if (a.pool_mode && b == 0 && tid < a.K) {
+        const int e = a.idx[tid];
+        if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+    }
     if (tab) {
         if (tid < a.K) {
             e_k = a.idx[tid];
@@ -443,7 +447,7 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
                 if ((uint32_t)(t[j] >> 32) != a.epoch) t[j] = fm_get_tagged(src + i);
             }
         } while (++it < FM_SPIN_MAX);
-        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
 #pragma unroll
         for (int j = 0; j < MAXQ; j++) {
             const uint32_t i = j * 256 + tid;
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
                 for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
                     if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)k * H + row]);
             } while (++it < FM_SPIN_MAX);
-            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
             const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
             const float yl = L.ylast[lane];
             float moe = 0.f;
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
                 while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
                     if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.ss2[lane]);
                 }
-                if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, 1u);
+                if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
                 const float part = lane < (int)tilesB ? __uint_as_float((uint32_t)v) : 0.f;
                 const float tot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(part))));
                 const float inv = 1.0f / sqrtf(tot / (float)H + a.norm_eps);

@@ -610,7 +610,7 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     for (int i = tid; i < n; i += blockDim.x) {
         int e = idx[i];
         if (e < 0 || e >= E) {
-            atomicOr(err, 1);
+            atomicOr(err, FM_STATUS_BAD_EXPERT);
             continue;
         }
         atomicAdd(&cnt[e], 1);
@@ -662,7 +662,7 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             base[NE] = ae;
             cbase[NE] = ac;
             *nchunks = ac <= (int)max_chunks ? ac : (int)max_chunks;
-            if (ac > (int)max_chunks) atomicOr(err, 2);
+            if (ac > (int)max_chunks) atomicOr(err, FM_STATUS_CHUNKS);
         }
     }
     __syncthreads();
@@ -774,13 +774,13 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     const size_t nent = (size_t)T * K + (has_shared ? T : 0);
     const uint32_t mc = pf_max_chunks(T, K, E, has_shared);
     size_t o = 0;
+    L.err = o;  // status word first (fm_workspace_status)
+    o += 256;
     L.entries = o;
     o += fm_align_up(nent * 4, 256);
     L.chunks = o;
     o += fm_align_up((size_t)mc * PF_CROW * 4, 256);
     L.nchunks = o;
-    o += 256;
-    L.err = o;
     o += 256;
     L.gout = o;
     o += fm_align_up(nent * inter * 4, 256);

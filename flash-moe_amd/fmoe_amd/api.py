@@ -15,8 +15,11 @@ __all__ = [
     "moe_decode", "moe_decode_pool", "encode_experts_batched", "moe_combine", "route_topk",
     "prefill_workspace_bytes", "prefill_moe", "pfb_gemm", "DevicePool", "moe_forward",
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
-    "moe_decode_pool_norm", "rms_norm", "moe_forward_norm",
+    "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
+    "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS",
 ]
+
+STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS = 1, 2, 4
 
 
 def _i32_array(vals):
@@ -95,6 +98,13 @@ def moe_decode_pool_norm(pool, idx, weights, x, out, ws, norm_w, eps, normed, sh
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
         shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(norm_w), float(eps),
         ptr(normed), ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def workspace_status(ws, stream=None):
+    """FM_STATUS_* bits accumulated in a decode/prefill workspace since the last call (then cleared)."""
+    v = ctypes.c_uint32()
+    check(lib().fm_workspace_status(ptr(ws), ctypes.byref(v), stream_ptr(stream)))
+    return v.value
 
 
 def rms_norm(x, w_bf16, eps, out, out_bf16=None, stream=None):

@@ -127,6 +127,18 @@ int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *
  * calls need their own. */
 size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
 
+/* Status word kept in the first 4 bytes of a decode or prefill workspace
+ * (fm_moe_decode*, fm_prefill_moe, fm_moe_forward*, fm_moe_prefill_forward):
+ * the kernels OR in FM_STATUS_* bits and never clear them.  This call waits for
+ * the work queued on `stream`, returns the accumulated bits in *status and
+ * clears them.  A freshly allocated workspace holds arbitrary bits: clear it
+ * once with this call before relying on it.  The reference only printed
+ * (e.g. "WARNING: expert %d pread" in expert_io.h:314); here the caller can ask. */
+#define FM_STATUS_WAIT_TIMEOUT 1u  /* a bounded wait between workgroups gave up: output invalid */
+#define FM_STATUS_BAD_EXPERT 2u    /* a routed expert index outside the pool was skipped */
+#define FM_STATUS_CHUNKS 4u        /* prefill: more expert chunks than the workspace holds */
+int fm_workspace_status(void *ws, uint32_t *status, void *stream);
+
 /* K expert FFNs sharing input x, one output per expert:
  *   expert_out[k] = down(silu(gate x) * up x)            [K][hidden] fp32
  * Replaces gpu_encode_experts_batched (gpu_dispatch.h:461-609): experts/bits

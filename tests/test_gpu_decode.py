@@ -343,3 +343,25 @@ def test_moe_decode_pool_large_expert_count(orc, dev):
     ref = orc.moe_decode([blobs[e % 8] for e in ri[0]], [bits[e % 8] for e in ri[0]], rw[0], x, HIDDEN, INTER,
                          h_mid=hm)
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+def test_workspace_status_bad_expert(orc, dev, pool64):
+    """An expert index outside the pool is skipped and reported (FM_STATUS_BAD_EXPERT);
+    a clean call reports nothing."""
+    import torch
+    say("workspace status")
+    blobs, bits, pool = pool64
+    K = 4
+    rng = synth.rng_for(43)
+    x = synth.hidden_vec(rng, HIDDEN)
+    ws = torch.empty(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.workspace_status(ws)  # a fresh workspace holds arbitrary bits
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    fm.moe_decode_pool(pool, T(np.array([3, 7, 11, 19], np.int32), dev), T(w, dev), T(x, dev), out, ws)
+    assert fm.workspace_status(ws) == 0
+    fm.moe_decode_pool(pool, T(np.array([3, 64, 11, -1], np.int32), dev), T(w, dev), T(x, dev), out, ws)
+    assert fm.workspace_status(ws) == fm.STATUS_BAD_EXPERT
+    ref = orc.moe_decode([blobs[3], blobs[11]], [bits[3], bits[11]], w[[0, 2]], x, HIDDEN, INTER)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+    assert fm.workspace_status(ws) == 0  # cleared by the previous read

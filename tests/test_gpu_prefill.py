@@ -160,3 +160,24 @@ def test_prefill_large_expert_count(orc, dev):
     ref = orc.prefill_moe(idx, w, [blobs8[e % 8] for e in range(E)], [bits8[e % 8] for e in range(E)], X, HIDDEN,
                           INTER)
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_prefill_status_bad_expert(orc, dev):
+    import torch
+    say("prefill status")
+    E, Tn, K = 16, 24, 3
+    bits = [4] * E
+    blobs = experts(range(3700, 3700 + E), bits)
+    pool = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    rng = synth.rng_for(44)
+    idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
+    X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
+    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
+    fm.workspace_status(ws)
+    fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws)
+    assert fm.workspace_status(ws) == 0
+    bad = idx.copy()
+    bad[5, 1] = E + 3
+    fm.prefill_moe(pool, T(bad, dev), T(w, dev), T(X, dev), out, ws)
+    assert fm.workspace_status(ws) == fm.STATUS_BAD_EXPERT

@@ -121,3 +121,10 @@ def test_zipf_routing_is_skewed(orc):
     idx, _ = orc.route(lg, 10)
     counts = np.bincount(idx.reshape(-1), minlength=512)
     assert counts.max() > 300 and np.median(counts[counts > 0]) < 10
+
+
+def test_workspace_status_rejects_null():
+    L = fmoe_amd.lib()
+    v = ctypes.c_uint32()
+    assert L.fm_workspace_status(None, ctypes.byref(v), None) == -1
+    assert b"NULL" in L.fm_last_error()
