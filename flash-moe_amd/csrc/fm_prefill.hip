@@ -502,7 +502,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
 // RES / VEC select one operand path and one scale-load path at compile time,
 // so the registers are sized for the path the launch takes.
 template <bool LO, bool DUAL, int NST, int W, bool RES, bool VEC>
-__global__ __launch_bounds__(64 * W, NST == 8 ? 1 : PF_MINB) void fm_pf_gemm_kernel(PfArgs a) {
+__global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_pf_gemm_kernel(PfArgs a) {
     __shared__ PfStage<LO> st[NST];
     __shared__ uint32_t tbuf[W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
@@ -996,9 +996,11 @@ __global__ void fm_pfb_lists_kernel(int N, int *entries, int *chunks, int *nchun
     if (i == 0) *nchunks = nc;
 }
 
+// [256 B left alone: the status word of a layer workspace that shares this
+// region][entries][chunk rows][nchunks], then the operands
 static size_t pfb_head(uint32_t N) {
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    return fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256) + 256;
+    return 256 + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256) + 256;
 }
 
 extern "C" size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim) {
@@ -1019,10 +1021,10 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     if ((uintptr_t)X & 15) return fm_fail(FM_ERR_INVALID, "%s: X not 16-byte aligned", who);
     if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     char *p = (char *)ws;
-    int *entries = (int *)p;
-    int *chunks = (int *)(p + fm_align_up((size_t)N * 4, 256));
+    int *entries = (int *)(p + 256);
+    int *chunks = (int *)(p + 256 + fm_align_up((size_t)N * 4, 256));
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    int *nchunks = (int *)(p + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256));
+    int *nchunks = (int *)(p + 256 + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256));
     hipStream_t st = fm_stream(stream);
     const uint32_t nt = (uint32_t)(N > nc ? N : nc);
     hipLaunchKernelGGL(fm_pfb_lists_kernel, dim3((nt + 255) / 256), dim3(256), 0, st, (int)N, entries, chunks, nchunks);

@@ -39,7 +39,9 @@ static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const
     if (!h_post || !out) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward: NULL h_post or out");
     size_t need = fm_moe_forward_workspace_size(L, K);
     if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_forward: workspace too small");
-    char *p = (char *)ws;
+    /* [decode step's workspace: status word first][logits][seg][idx][w] */
+    const size_t step = fm_moe_decode_workspace_size(K + 1, L->pool.hidden, L->pool.inter);
+    char *p = (char *)ws + step;
     float *logits = (float *)p;
     p += align256((size_t)L->pool.num_experts * sizeof(float));
     float *seg = (float *)p;
@@ -47,8 +49,8 @@ static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const
     int *idx = (int *)p;
     p += align256((size_t)K * sizeof(int));
     float *w = (float *)p;
-    p += align256((size_t)K * sizeof(float));
-    size_t rest = ws_bytes - (size_t)(p - (char *)ws);
+    p = (char *)ws;
+    size_t rest = step;
 
     /* CMD2: routing gate (+ shared_expert_gate) share h_post (3506-3512) */
     fm_batch_matvec_spec specs[2] = {
@@ -94,7 +96,7 @@ size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
     n += align256((size_t)T * K * sizeof(float));
     size_t g1 = fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden);
     size_t g2 = fm_prefill_moe_workspace_size(T, K, &L->pool);
-    return n + (g1 > g2 ? g1 : g2);
+    return n + align256(g1 > g2 ? g1 : g2);
 }
 
 int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
@@ -104,7 +106,11 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     if (T <= 0 || !h_post || !out) return fm_host_fail(FM_ERR_INVALID, "fm_moe_prefill_forward: T <= 0 or NULL buffer");
     size_t need = fm_moe_prefill_workspace_size(L, K, T);
     if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_prefill_forward: workspace too small");
-    char *p = (char *)ws;
+    /* [router GEMM / expert step region: status word first][logits][seg][idx][w] */
+    size_t g1 = fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden);
+    size_t g2 = fm_prefill_moe_workspace_size(T, K, &L->pool);
+    const size_t step = align256(g1 > g2 ? g1 : g2);
+    char *p = (char *)ws + step;
     float *logits = (float *)p;
     p += align256((size_t)T * L->pool.num_experts * sizeof(float));
     float *seg = (float *)p;
@@ -112,8 +118,8 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     int *idx = (int *)p;
     p += align256((size_t)T * K * sizeof(int));
     float *w = (float *)p;
-    p += align256((size_t)T * K * sizeof(float));
-    size_t rest = ws_bytes - (size_t)(p - (char *)ws);
+    p = (char *)ws;
+    size_t rest = step;
 
     /* routing gate and shared_expert_gate over all tokens (batched_prefill.h:164-182) */
     int rc = fm_pfb_gemm(L->router_w, L->router_s, L->router_b, h_post, logits, (uint32_t)T,

@@ -227,6 +227,7 @@ def test_moe_forward_layer(orc, dev, pool64):
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_forward(L, K, T(hp, dev), T(hm, dev), out, ws)
     torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0  # the step's status word sits at the start of the layer workspace
     logits = orc.matvec(4, Wr, sr, br, hp)
     score = orc.matvec(4, Wg, sg, bg, hp)[0]
     ri, rw = orc.route(logits, K)

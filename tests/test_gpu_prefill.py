@@ -131,6 +131,7 @@ def test_moe_prefill_forward_layer(orc, dev):
     out = torch.empty((Tn, H), dtype=torch.float32, device=dev)
     fm.moe_prefill_forward(L, K, Tn, T(X, dev), T(hm, dev), out, ws)
     torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
     logits = orc.gemm(4, Wr, sr, br, X)
     scores = orc.gemm(4, Wg, sg, bg, X)[:, 0]
     idx, w = orc.route(logits, K)
