@@ -282,6 +282,78 @@ def bench_tiered(args, dev):
     return res
 
 
+def bench_small(args, dev, pool):
+    """Configs 0 and 1: one 4096x4096 4-bit matvec (fm_dequant_matvec) and one
+    SwiGLU expert scaled by a router weight (fm_moe_decode, K = 1), back-to-back
+    launches rotating over more weights than the 256 MB MALL holds (32 matrix
+    copies; the 512-expert pool)."""
+    import numpy as np
+    import torch
+    import fmoe_amd as fm
+    from fmoe_amd import synth
+    n = 32
+    W, sc, bi = synth.quant_matrix(synth.rng_for(3300), 4096, 4096, 4)
+    dW = torch.from_numpy(W).to(dev)
+    ds = torch.from_numpy(sc.view(np.int16)).to(dev)
+    db = torch.from_numpy(bi.view(np.int16)).to(dev)
+    copies = [(dW.clone(), ds.clone(), db.clone()) for _ in range(n)]
+    x = torch.from_numpy(synth.hidden_vec(synth.rng_for(3301), 4096)).to(dev)
+    y = torch.empty(4096, dtype=torch.float32, device=dev)
+    steps = max(args.steps, 100)
+    # arguments built once and the C entry points called directly, so the
+    # launches outpace the GPU (a Python wrapper per call would not)
+    import ctypes
+    L = fm.lib()
+    sp = fm.stream_ptr()
+    mv_args = [(c[0].data_ptr(), c[1].data_ptr(), c[2].data_ptr()) for c in copies]
+    xp, yp = x.data_ptr(), y.data_ptr()
+
+    def mv(i):
+        w_, s_, b_ = mv_args[i % n]
+        return L.fm_dequant_matvec(w_, s_, b_, xp, yp, 4096, 4096, 64, 4, sp)
+
+    for i in range(10):
+        fm.check(mv(i))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        mv(i)
+    e1.record()
+    torch.cuda.synchronize()
+    mv_us = e0.elapsed_time(e1) * 1e3 / steps
+    mv_bytes = 4096 * 512 * 4 + 2 * 4096 * 64 * 2 + 4096 * 2 + 4096 * 4
+    ws = torch.zeros(fm.decode_workspace_bytes(1, H, I), dtype=torch.uint8, device=dev)
+    out = torch.empty(H, dtype=torch.float32, device=dev)
+    ex_args = []
+    for e in range(E):
+        arr = (fm.ExpertWeights * 1)(pool.expert(e))
+        ex_args.append(arr)
+    bits1, w1 = (ctypes.c_int * 1)(4), (ctypes.c_float * 1)(0.37)
+    wsp, wsb, outp = ws.data_ptr(), ws.numel(), out.data_ptr()
+
+    def ex(i):
+        return L.fm_moe_decode(1, ex_args[(i * 37) % E], bits1, w1, None, None, 4, 0.0, H, I, 64, xp, None, outp,
+                               None, wsp, wsb, sp)
+
+    for i in range(10):
+        fm.check(ex(i))
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        ex(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ex_us = e0.elapsed_time(e1) * 1e3 / steps
+    ex_bytes = fm.layout_of(H, I, 64, 4).size + H * 2 + H * 4
+    return {"config0_matvec": {"workload": "4096x4096 4-bit g64 matvec, 32 rotating copies", "us": round(mv_us, 2),
+                               "bytes": mv_bytes, "gbs": round(mv_bytes / mv_us / 1e3, 1),
+                               "hbm_frac": round(mv_bytes / mv_us / 1e3 / HBM_PEAK_GBS, 4)},
+            "config1_expert": {"workload": "one 4096->1024->4096 4-bit SwiGLU expert x router weight, 512 rotating",
+                               "us": round(ex_us, 2), "bytes": ex_bytes, "gbs": round(ex_bytes / ex_us / 1e3, 1),
+                               "hbm_frac": round(ex_bytes / ex_us / 1e3 / HBM_PEAK_GBS, 4)}}
+
+
 def bench_staging(args, dev):
     """Expert files -> HBM (fm_expert_io.h), from a warm page cache: a whole layer
     file loaded into device memory, and per-token staging of K+1 experts
@@ -421,6 +493,9 @@ def main():
     log(f"decode: {dec['step_ms'] * 1e3:.2f} us/step, {dec['value']:.0f} GB/s; fused launch "
         f"{dec['roofline']['kernel_us']:.2f} us = {dec['roofline']['achieved']:.0f} GB/s; whole MoE block "
         f"(router + routing + experts) {dec['layer_step']['us']} us")
+    small = bench_small(args, dev, args._pool)
+    log(f"config 0 matvec: {small['config0_matvec']['us']} us = {small['config0_matvec']['gbs']} GB/s; "
+        f"config 1 expert: {small['config1_expert']['us']} us = {small['config1_expert']['gbs']} GB/s")
     pre = None if args.no_prefill else bench_prefill(args, dev, args._pool)
     if pre:
         log(f"prefill: {pre['ms']:.3f} ms/layer, {pre['tokens_per_s']:.0f} tok/s, {pre['hbm_gbs']:.0f} GB/s, "
@@ -445,6 +520,7 @@ def main():
                    "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"]},
         "roofline": dec["roofline"],
         "layer_step": dec["layer_step"],
+        "single": small,
         "prefill": None if pre is None else {
             "workload": "config 3: 512 tokens, 512 experts, top-10 Zipf(1.1) + shared, grouped MFMA dequant-GEMM",
             "tokens_per_s": round(pre["tokens_per_s"]), "ms_per_layer": pre["ms"],

@@ -5,8 +5,9 @@
 //
 // Mapping: 64-lane wavefront; LPR lanes share one output row, each lane owns
 // whole 64-element groups (32 B of packed 4-bit codes = two 128-bit loads,
-// one bf16 scale, one bf16 bias).  The lane's slice of x lives in VGPRs as
-// fp16 pairs for the whole kernel, so x is read once per wave, not per row.
+// one bf16 scale, one bf16 bias).  A wave issues all of its weight loads
+// first; the workgroup then stages x once in LDS as fp16 pairs in the operand
+// layout of every group (a per-lane copy would read all of x per wave).
 // Rows are reduced across the LPR lanes with cross-lane adds; fp32 throughout.
 // Several matvecs sharing x (a BatchMatvecSpec list) go in ONE launch: the
 // block index is mapped to (spec, row block) through a prefix table.
@@ -36,7 +37,7 @@ struct FmMvArgs {
 
 template <int BITS, int LPR, int GPL>
 __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__restrict__ x,
-                                           uint32_t in_dim, uint32_t row0) {
+                                           uint32_t in_dim, uint32_t row0, FmXGroup *xs) {
     constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, gl = lane % LPR;
@@ -44,13 +45,7 @@ __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__re
     const uint32_t wpr = in_dim * BITS / 32;  // u32 words per row
     constexpr int WPG = 2 * BITS;              // words per group
 
-    FmXGroup xg[GPL];
-#pragma unroll
-    for (int j = 0; j < GPL; j++) {
-        uint32_t g = gl + j * LPR;
-        if (g < G) fm_load_xgroup<BITS>(x + 64 * g, xg[j]);
-    }
-
+    // weights first: all of this wave's rows in flight before x is staged
     FmWGroup wv[FM_MV_NP][GPL];
     float sv[FM_MV_NP][GPL], bv[FM_MV_NP][GPL];
 #pragma unroll
@@ -66,6 +61,9 @@ __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__re
             }
         }
     }
+    // x once per workgroup, as the lane operand layout of every group, in LDS
+    for (uint32_t g = threadIdx.x; g < G; g += blockDim.x) fm_load_xgroup<BITS>(x + 64 * g, xs[g]);
+    __syncthreads();
 #pragma unroll
     for (int p = 0; p < FM_MV_NP; p++) {
         uint32_t row = row0 + p * RPP + sub;
@@ -73,7 +71,7 @@ __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__re
 #pragma unroll
         for (int j = 0; j < GPL; j++) {
             uint32_t g = gl + j * LPR;
-            if (row < sp.out_dim && g < G) part += fm_group_dot<BITS>(wv[p][j], xg[j], sv[p][j], bv[p][j]);
+            if (row < sp.out_dim && g < G) part += fm_group_dot<BITS>(wv[p][j], xs[g], sv[p][j], bv[p][j]);
         }
         float tot = fm_lane_sum<LPR>(part);
         if (gl == 0 && row < sp.out_dim) sp.out[row] = tot;
@@ -84,15 +82,16 @@ template <int LPR, int GPL>
 __global__ __launch_bounds__(256) void fm_matvec_kernel(FmMvArgs a) {
     constexpr int RPP = 64 / LPR;
     constexpr int RB = 4 * FM_MV_NP * RPP;  // rows per block
+    __shared__ FmXGroup xs[256];            // in_dim <= 16384
     const uint32_t blk = blockIdx.x;
     int si = 0;
     while (si + 1 < a.nspec && blk >= a.spec[si + 1].block_start) si++;
     const FmMvSpec &sp = a.spec[si];
     const uint32_t row0 = (blk - sp.block_start) * RB + (threadIdx.x >> 6) * (FM_MV_NP * RPP);
     if (sp.bits == 4)
-        fm_mv_body<4, LPR, GPL>(sp, a.x, a.in_dim, row0);
+        fm_mv_body<4, LPR, GPL>(sp, a.x, a.in_dim, row0, xs);
     else
-        fm_mv_body<2, LPR, GPL>(sp, a.x, a.in_dim, row0);
+        fm_mv_body<2, LPR, GPL>(sp, a.x, a.in_dim, row0, xs);
 }
 
 static int fm_launch_matvec(const FmMvArgs &a, int lpr, int gpl, uint32_t blocks, hipStream_t st) {
