@@ -277,7 +277,7 @@ def bench_tiered(args, dev):
         res[f"b{B}"] = {"us_per_step": ms * 1e3, "bytes_per_step": round(step_bytes),
                         "gbs": step_bytes / (ms * 1e-3) / 1e9,
                         "hbm_frac": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                        "path": "route + fm_moe_decode_pool" if B == 1 else "route + fm_prefill_moe (T <= 8: one fused decode step per token)"}
+                        "path": "route + fm_moe_decode_pool" if B == 1 else "route + fm_prefill_moe (few tokens: all tokens' slots in one multi-pass decode launch)"}
     del pool
     return res
 

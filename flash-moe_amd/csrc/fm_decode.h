@@ -17,8 +17,10 @@ struct FmSlot {
 
 struct FmDecodeArgs {
     FmSlot slot[FM_MAX_SLOTS];
-    int S;          // slots in use (K routed + optional shared)
-    int K;          // routed slots
+    int S;          // slots in use: ntok x spt
+    int K;          // routed slots per token
+    int ntok;       // tokens of the launch (mfma kernel, pool mode); others: 1
+    int spt;        // slots per token (K + has_shared)
     int has_shared; // slot K is the shared expert
     int pool_mode;  // routed slots resolved from pool + idx on the device
     int mode;       // 0: combine into out; 1: per-slot outputs (expert_out)
@@ -49,10 +51,11 @@ struct FmDecodeArgs {
     uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
 };
 
-__device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
+// Slot k of token tok (routed slots of token tok read idx/wdev row tok).
+__device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k, int tok = 0) {
     if (!a.pool_mode || k >= a.K) return a.slot[k];
     FmSlot s;
-    int e = a.idx[k];
+    int e = a.idx[tok * a.K + k];
     if (e < 0 || (uint32_t)e >= a.pool_n) {
         s.valid = 0;
         s.bits = 4;
@@ -72,7 +75,7 @@ __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k) {
     s.ds = (const uint16_t *)(blob + off[7]);
     s.db = (const uint16_t *)(blob + off[8]);
     s.bits = bits;
-    s.weight = a.wdev[k];
+    s.weight = a.wdev[tok * a.K + k];
     s.valid = blob != nullptr && (bits == 2 || bits == 4);
     return s;
 }

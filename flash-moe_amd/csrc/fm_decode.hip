@@ -750,6 +750,10 @@ static bool fm_decode_allowed(const char *name) {
 
 static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const char *who = "fm_moe_decode";
+    if (a.ntok <= 1) {
+        a.ntok = 1;
+        a.spt = a.S;
+    }
     FM_REQUIRE(a.hidden % 64 == 0 && a.inter % 64 == 0 && a.hidden && a.inter,
                "%s: hidden %u / inter %u must be positive multiples of 64", who, a.hidden, a.inter);
     size_t need = fm_moe_decode_workspace_size(a.S, a.hidden, a.inter);
@@ -767,6 +771,9 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     p += fm_align_up((size_t)a.S * a.hidden * 8, 256);
     a.ss2 = (uint64_t *)p;
     a.epoch = fm_next_epoch();
+    if (a.ntok > 1)  // several tokens in one launch: only the mfma kernel implements it
+        return fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st)
+                                         : fm_fail(FM_ERR_UNSUPPORTED, "%s: several tokens need the mfma kernel", who);
     if (a.norm_w) {
         // the fused kernels normalise in their combine; every other path runs
         // the standalone norm after the step
@@ -845,11 +852,13 @@ extern "C" int fm_moe_decode(int K, const fm_expert_weights *experts, const int 
     return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
 }
 
+// T tokens (rows of idx/weights/x/h_mid/out/out_bf16, entries of
+// shared_gate_score) in one launch; T > 1 only through fm_moe_decode_pool_tokens.
 static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int K, const int *idx,
                                const float *weights, const fm_expert_weights *shared, int shared_bits,
                                const float *shared_gate_score, const float *x, const float *h_mid, float *out,
                                uint16_t *out_bf16, const uint16_t *norm_w, float norm_eps, float *normed, void *ws,
-                               size_t ws_bytes, void *stream) {
+                               size_t ws_bytes, void *stream, int T = 1) {
     FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
     FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
     FM_REQUIRE(K == 0 || (idx && weights), "%s: NULL idx/weights", who);
@@ -890,7 +899,24 @@ static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int 
     a.h_mid = h_mid;
     a.out = out;
     a.out_bf16 = out_bf16;
+    if (T > 1) {
+        a.ntok = T;
+        a.spt = a.S;
+        a.S = T * a.spt;
+    }
     return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
+}
+
+size_t fm_moe_decode_tokens_workspace_size(int T, int K, int has_shared, uint32_t hidden, uint32_t inter) {
+    return fm_moe_decode_workspace_size(T * (K + has_shared), hidden, inter);
+}
+
+int fm_moe_decode_pool_tokens(const fm_expert_pool *pool, int T, int K, const int *idx, const float *weights,
+                              const fm_expert_weights *shared, int shared_bits, const float *shared_gate_scores,
+                              const float *X, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
+                              size_t ws_bytes, void *stream) {
+    return fm_decode_pool_impl("fm_prefill_moe", pool, K, idx, weights, shared, shared_bits, shared_gate_scores, X,
+                               h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream, T);
 }
 
 extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx, const float *weights,

@@ -48,8 +48,10 @@ typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
 #define FM_DX_MARK(n)
 #endif
 
+#define FMM_MAXS 64   // slots of one launch (tokens x slots per token)
 #define FMM_TAB 1024  // pools up to this many experts: the blob/bits tables are staged in LDS
 
+template <int NSLOT>  // slot table entries (the one-pass instance needs few: keeps 3 blocks per CU)
 struct __attribute__((aligned(16))) FmmLds {
     fm_h2 xq[2][FMM_GH][32];  // x as MFMA operand rows: [4-bit | 2-bit layout][group][32 pairs]
     fm_h2 aq[2][FMM_GI][32];  // the B slot's activations, same layouts
@@ -65,7 +67,7 @@ struct __attribute__((aligned(16))) FmmLds {
     float part[4][16][2];     // per-wave partial gate/up sums of the A rows
     float ylast[64];          // this block's rows of the last slot's y
     uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
-    FmSlot sd[FM_MAX_SLOTS];
+    FmSlot sd[NSLOT];
 };
 
 // fm_pool_slot with the blob / bits tables read from their LDS copies.
@@ -162,9 +164,9 @@ struct FmmCodes {
 // scale/bias runs follow the MFMA layout: lane (n, kq) takes row row0 + n,
 // groups g0 + 4kq .. g0 + 4kq + 3.
 FM_DEV void fmm_issue(const uint32_t *W, const uint16_t *S, const uint16_t *B, int bits, uint32_t row0,
-                      uint32_t in_dim, uint32_t g0, bool ok, FmmCodes &cd, fmm_u2 &sc, fmm_u2 &bi) {
+                      uint32_t in_dim, uint32_t g0, bool ok, FmmCodes &cd, fmm_u2 &sc, fmm_u2 &bi, int lane) {
     if (!ok) return;
-    const int lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const int n = lane & 15, kq = lane >> 4;
     const uint32_t G = in_dim / 64;
     const uint32_t wpg = 2 * bits;  // words per group
     const uint32_t wpr = G * wpg;   // words per row
@@ -194,8 +196,8 @@ FM_DEV uint32_t fmm_comp(const fm_u4 &v, int j) { return j == 0 ? v.x : j == 1 ?
 // j; scheduling barriers keep the compiler from hoisting further reads.
 template <int BITS>
 FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, uint32_t *T, fmm_f4 &d0,
-                    fmm_f4 &d1) {
-    const int lane = threadIdx.x & 63, m = lane & 15, kq = lane >> 4;
+                    fmm_f4 &d1, int lane) {
+    const int m = lane & 15, kq = lane >> 4;
     auto src_of = [&](int j) -> const fm_h2 * {
         const int c = j >> 3, i = j & 7;
         if constexpr (BITS == 4) {
@@ -290,42 +292,76 @@ FM_DEV float fmm_q_sum(float v) {
     return v;
 }
 
-__global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(FmDecodeArgs a) {
-    __shared__ FmmLds L;
+// A slot descriptor read from LDS is the same in every lane: keep it in scalar registers.
+FM_DEV FmSlot fmm_uniform(const FmSlot &v) {
+    FmSlot r;
+    const uint32_t *src = (const uint32_t *)&v;
+    uint32_t *dst = (uint32_t *)&r;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(FmSlot) / 4); i++) dst[i] = __builtin_amdgcn_readfirstlane(src[i]);
+    return r;
+}
+
+typedef __attribute__((address_space(4))) const FmDecodeArgs FmmCArgs;
+// The launch arguments in the kernarg segment, opaque to the optimiser.
+FM_DEV const FmDecodeArgs *fmm_args() {
+    FmmCArgs *p = (FmmCArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return (const FmDecodeArgs *)p;
+}
+
+// MP (multi-pass): the grid is smaller than the work and blocks loop over
+// items; the loop costs the compiler ~24 registers, so that instance runs two
+// blocks per CU (no spills) while the one-pass instance keeps three.
+template <bool MP>
+__global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(FmDecodeArgs a_) {
+    const FmDecodeArgs &a = a_;
+    __shared__ FmmLds<MP ? FMM_MAXS : FM_MAX_SLOTS> L;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, q = lane >> 4;
     const uint32_t H = a.hidden, I = a.inter;
     const uint32_t GI = I / 64;
     const uint32_t tilesA = I / 16, tilesB = H / 64;
-    const uint32_t b = blockIdx.x;
-    const bool hasA = b < (uint32_t)a.S * tilesA;
-    const bool hasB = b < (uint32_t)a.S * tilesB;
-    const int kA = hasA ? (int)(b / tilesA) : 0;
-    const int kB = hasB ? (int)(b / tilesB) : 0;
+    const int spt = a.spt;
+    // Work items: item i is A tile i and B tile i (slot i / tiles).  The grid
+    // is a whole number of slots' tiles and every block takes items b, b + grid,
+    // ...: the items of one slot always run in the same pass, so a block only
+    // ever waits for blocks that are resident in that pass (or done).
+    const uint32_t nitems = (uint32_t)a.S * (tilesA > tilesB ? tilesA : tilesB);
+    const uint32_t b0 = blockIdx.x;
+    auto token_of = [&](uint32_t item) -> int {
+        const uint32_t k = item / tilesA;
+        return (int)((k < (uint32_t)a.S ? k : 0) / spt);
+    };
 
     FM_DX_MARK(0);
     // x first: thread t holds elements 16*(t%4) .. +15 of group t/4.  Loaded
     // before the slot lookup and the weights, so its latency overlaps theirs.
     fm_f4 xr[4];
-    {
-        const float *xp = a.x + 16 * tid;
+    auto load_x = [&](uint32_t item) {
+        const float *xp = a.x + (size_t)token_of(item) * H + 16 * tid;
 #pragma unroll
         for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(xp + 4 * j);
-    }
-    // Slots.  A pool of up to FMM_TAB experts has its blob/bits tables staged
-    // in LDS together with idx / weights (independent loads, one round trip)
-    // instead of the dependent chain idx -> table entry.
+    };
+    load_x(b0);
+    // Slots of every token.  A pool of up to FMM_TAB experts has its blob/bits
+    // tables staged in LDS together with idx / weights (independent loads, one
+    // round trip) instead of the dependent chain idx -> table entry.
     const bool tab = a.pool_mode && a.pool_n <= FMM_TAB;
+    const int sT = tid < a.S ? tid / spt : 0, sK = tid < a.S ? tid % spt : 0;
+    const bool routed = tid < a.S && sK < a.K;
     int e_k = 0;
     float w_k = 0.f;
-    if (a.pool_mode && b == 0 && tid < a.K) {
-        const int e = a.idx[tid];
-        if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+    if (a.pool_mode && b0 == 0) {
+        for (int i = tid; i < a.ntok * a.K; i += 256) {
+            const int e = a.idx[i];
+            if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+        }
     }
     if (tab) {
-        if (tid < a.K) {
-            e_k = a.idx[tid];
-            w_k = a.wdev[tid];
+        if (routed) {
+            e_k = a.idx[sT * a.K + sK];
+            w_k = a.wdev[sT * a.K + sK];
         }
         for (uint32_t e = tid; e < a.pool_n; e += 256) {
             const char *p = (const char *)a.pool_blobs[e];
@@ -336,25 +372,44 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
             L.tbits[e] = a.pool_bits[e];
         }
         __syncthreads();
-        if (tid < a.K) {
+        if (routed) {
             L.sd[tid] = fm_pool_slot_tab(a, e_k, w_k, L.tab, L.tab2, L.tbits);
         } else if (tid < a.S) {
-            L.sd[tid] = a.slot[tid];
+            L.sd[tid] = a.slot[sK];
         }
     } else if (tid < a.S) {
-        L.sd[tid] = fm_get_slot(a, tid);
+        L.sd[tid] = fm_get_slot(a, sK, sT);
     }
     if (tid < 32) L.zero[tid] = fm_as_h2(0u);
     __syncthreads();
-    const FmSlot sA = L.sd[kA], sB = L.sd[kB];
-    const int ph = a.phases ? a.phases : 3;
-    const bool doA = (ph & 1) && hasA && sA.valid, doB = (ph & 2) && hasB && sB.valid;
+
+    for (uint32_t b = b0; b < nitems; b += gridDim.x) {
+    // The arguments are re-read from the kernarg segment per item (scalar
+    // loads): hoisted out of the loop they would all stay live in registers.
+    const FmDecodeArgs &a = MP ? *fmm_args() : a_;
+    // the thread index is made opaque per item too, so that no per-lane
+    // address arithmetic is hoisted out of the loop
+    int tid = threadIdx.x;
+    if constexpr (MP) asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wv = tid >> 6, n = lane & 15, q = lane >> 4;
+    const int spt = a.spt, ph = a.phases ? a.phases : 3;
+    const uint32_t H = a.hidden, I = a.inter, GI = I / 64, tilesA = I / 16, tilesB = H / 64;
+    if (b != b0) load_x(b);
+    const bool hasA = b < (uint32_t)a.S * tilesA;
+    const bool hasB = b < (uint32_t)a.S * tilesB;
+    const int kA = hasA ? (int)(b / tilesA) : 0;
+    const int kB = hasB ? (int)(b / tilesB) : 0;
+    const int tokB = kB / spt;  // token of the B slot (the combine's token)
+    const FmSlot sA = MP ? fmm_uniform(L.sd[kA]) : L.sd[kA];
+    FmSlot sB;
+    if constexpr (!MP) sB = L.sd[kB];
+    const bool doA = (ph & 1) && hasA && sA.valid;
     // ---- issue every weight load of this wave ----
     const uint32_t rowA0 = (b % tilesA) * 16;
     FmmCodes cg, cu, cdn;
     fmm_u2 sg = {0, 0}, bg = {0, 0}, su = {0, 0}, bu = {0, 0}, sdn = {0, 0}, bdn = {0, 0};
-    fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg);
-    fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu);
+    fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg, lane);
+    fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu, lane);
     const uint32_t rowB0 = (b % tilesB) * 64 + 16 * wv;
 
     FM_DX_MARK(1);
@@ -396,11 +451,11 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[sA.bits == 4 ? 0 : 1][16 * wv][0];
         if (sA.bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1);
-            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1);
+            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         } else {
-            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1);
-            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1);
+            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         }
         const float *gs4 = &L.xsum[16 * wv + 4 * q];
         float pg = fmm_fold(g0 + g1, sg, bg, gs4);
@@ -424,7 +479,9 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     // Down-projection loads are issued only now: their data is useless before
     // the slot's activations exist, and issuing them early would only delay
     // other waves' gate/up data.
-    fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn);
+    if constexpr (MP) sB = fmm_uniform(L.sd[kB]);  // read only now: fewer registers live during A
+    const bool doB = (ph & 2) && hasB && sB.valid;
+    fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn, lane);
     // ---- B: stage the slot's activations, then 16 down rows per wave ----
     if (doB) {
         constexpr int MAXQ = FMM_MAXI / 256;
@@ -468,14 +525,14 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     }
     __syncthreads();
     FM_DX_MARK(5);
-    const bool last = (ph & 2) && hasB && a.mode == 0 && kB == a.S - 1;
+    const bool last = (ph & 2) && hasB && a.mode == 0 && kB % spt == spt - 1;
     if (doB) {
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &L.aq[sB.bits == 4 ? 0 : 1][0][0];
         if (sB.bits == 4)
-            fmm_mma<4>(cdn, aq, L.zero, L.tr[wv], d0, d1);
+            fmm_mma<4>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         else
-            fmm_mma<2>(cdn, aq, L.zero, L.tr[wv], d0, d1);
+            fmm_mma<2>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q]);
         y = fmm_q_sum(y);
         const uint32_t row = rowB0 + n;
@@ -492,18 +549,19 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
     }
 
     FM_DX_MARK(6);
-    // ---- C: the last slot's blocks combine their 64 rows over all slots ----
+    // ---- C: the blocks of a token's last slot combine their 64 rows over the token's slots ----
     if (last) {
         __syncthreads();
         if (wv == 0) {
             // one wavefront gathers every other slot's y for the 64 rows with
             // one batch of coherent loads, re-polling only what is not ready
             const uint32_t row = (b % tilesB) * 64 + lane;
+            const int k0 = tokB * spt;  // the token's first slot
             uint64_t t[FM_MAX_SLOTS - 1];
 #pragma unroll
             for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
-                t[k] = (k < a.S - 1 && L.sd[k].valid) ? fm_get_tagged(&a.y2[(size_t)k * H + row])
-                                                     : ((uint64_t)a.epoch << 32);
+                t[k] = (k < spt - 1 && L.sd[k0 + k].valid) ? fm_get_tagged(&a.y2[(size_t)(k0 + k) * H + row])
+                                                         : ((uint64_t)a.epoch << 32);
             uint32_t it = 0;
             do {
                 bool ready = true;
@@ -512,23 +570,25 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
                 if (__all(ready)) break;
 #pragma unroll
                 for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
-                    if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)k * H + row]);
+                    if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)(k0 + k) * H + row]);
             } while (++it < FM_SPIN_MAX);
             if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
-            const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+            const float sw =
+                a.has_shared ? (a.shared_score ? fm_sigmoid(a.shared_score[tokB]) : a.shared_w_host) : 0.f;
             const float yl = L.ylast[lane];
             float moe = 0.f;
 #pragma unroll
             for (int k = 0; k < FM_MAX_SLOTS; k++) {
-                if (k < a.K && L.sd[k].valid) {
-                    const float yk = k == a.S - 1 ? yl : __uint_as_float((uint32_t)t[k < FM_MAX_SLOTS - 1 ? k : 0]);
-                    moe = __fadd_rn(moe, __fmul_rn(L.sd[k].weight, yk));
+                if (k < a.K && L.sd[k0 + k].valid) {
+                    const float yk = k == spt - 1 ? yl : __uint_as_float((uint32_t)t[k < FM_MAX_SLOTS - 1 ? k : 0]);
+                    moe = __fadd_rn(moe, __fmul_rn(L.sd[k0 + k].weight, yk));
                 }
             }
-            float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+            const size_t orow = (size_t)tokB * H + row;
+            float o = a.h_mid ? __fadd_rn(a.h_mid[orow], moe) : moe;
             if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, yl));
-            a.out[row] = o;
-            if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+            a.out[orow] = o;
+            if (a.out_bf16) a.out_bf16[orow] = fm_f32_to_bf16(o);
             if (a.norm_w) {
                 // next layer's input RMS norm (cpu_kernels.h:235-246): every
                 // combining block publishes the sum of squares of its 64 rows,
@@ -550,21 +610,38 @@ __global__ __launch_bounds__(256, FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(
         }
     }
     FM_DX_MARK(7);
+    __syncthreads();  // LDS of this item is reused by the next
+    if constexpr (!MP) break;
+    }
 }
 
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
     if (a.hidden != FMM_H || a.inter != FMM_MAXI)
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: shape");
-    static int per_cu = -1;
+    static int per_cu = -1, per_cu_mp = -1;
     if (per_cu < 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_mfma_kernel, 256, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_mfma_kernel<false>, 256, 0) != hipSuccess)
             per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_mp, fm_decode_mfma_kernel<true>, 256, 0) !=
+            hipSuccess)
+            per_cu_mp = 0;
     }
-    const uint32_t nA = (uint32_t)a.S * (a.inter / 16), nB = (uint32_t)a.S * (a.hidden / 64);
-    const uint32_t blocks = nA > nB ? nA : nB;
-    // every block may wait on others: the whole grid must be resident
-    if (per_cu < 1 || blocks > (uint32_t)(per_cu * fm_num_cus())) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: grid");
-    hipLaunchKernelGGL(fm_decode_mfma_kernel, dim3(blocks), dim3(256), 0, st, a);
+    if (a.S > FMM_MAXS || a.spt < 1 || a.S != a.ntok * a.spt)
+        return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
+    if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
+        return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
+    const uint32_t tiles = a.inter / 16 > a.hidden / 64 ? a.inter / 16 : a.hidden / 64;
+    const uint32_t items = (uint32_t)a.S * tiles;
+    // every block may wait on others: the grid must be resident, and it is a
+    // whole number of slots so that a slot's tiles run in one pass
+    const uint32_t cap = per_cu > 0 ? (uint32_t)(per_cu * fm_num_cus()) / tiles * tiles : 0;
+    if (items <= cap && a.S <= FM_MAX_SLOTS) {
+        hipLaunchKernelGGL(fm_decode_mfma_kernel<false>, dim3(items), dim3(256), 0, st, a);
+        return fm_check_launch("fm_decode_mfma_kernel");
+    }
+    const uint32_t cap_mp = per_cu_mp > 0 ? (uint32_t)(per_cu_mp * fm_num_cus()) / tiles * tiles : 0;
+    if (cap_mp == 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: grid");
+    hipLaunchKernelGGL(fm_decode_mfma_kernel<true>, dim3(cap_mp), dim3(256), 0, st, a);
     return fm_check_launch("fm_decode_mfma_kernel");
 }

@@ -128,6 +128,7 @@ struct FmWGroup {
 // in-flight weight prefetches.  These force global_load_* instead.
 #define FM_GLOBAL __attribute__((address_space(1)))
 FM_DEV fm_u4 fm_ldg_u4_nt(const void *p) { return __builtin_nontemporal_load((const FM_GLOBAL fm_u4 *)p); }
+FM_DEV fm_u4 fm_ldg_u4(const void *p) { return *(const FM_GLOBAL fm_u4 *)p; }
 FM_DEV uint16_t fm_ldg_u16(const void *p) { return *(const FM_GLOBAL uint16_t *)p; }
 FM_DEV float fm_ldg_f32(const void *p) { return *(const FM_GLOBAL float *)p; }
 FM_DEV fm_f4 fm_ldg_f4(const void *p) { return *(const FM_GLOBAL fm_f4 *)p; }

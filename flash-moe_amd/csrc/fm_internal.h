@@ -41,3 +41,13 @@ int fm_check_dims(const char *who, uint32_t out_dim, uint32_t in_dim, uint32_t g
 
 // Compute units of the current device (cached per device).
 int fm_num_cus(void);
+
+// T tokens' decode steps in one launch of the mfma decode kernel (pool mode):
+// rows t of idx/weights [T][K], X/h_mid/out/out_bf16 [T][hidden] and
+// shared_gate_scores[t].  FM_ERR_UNSUPPORTED (message set) when that kernel
+// cannot take the shape or T x (K + shared) slots.
+size_t fm_moe_decode_tokens_workspace_size(int T, int K, int has_shared, uint32_t hidden, uint32_t inter);
+int fm_moe_decode_pool_tokens(const fm_expert_pool *pool, int T, int K, const int *idx, const float *weights,
+                              const fm_expert_weights *shared, int shared_bits, const float *shared_gate_scores,
+                              const float *X, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
+                              size_t ws_bytes, void *stream);

@@ -36,7 +36,7 @@ typedef float fm_f4v __attribute__((ext_vector_type(4)));
 #define PF_TOK 16    // token columns per MFMA N tile
 #define PF_CROW 32   // ints per chunk row: expert, entry offset, count, bits, blob address (2), pad, 16 slot ids
 #define PF_CHUNK PF_TOK  // entries per chunk (one block covers a chunk x 64 rows)
-#define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: one fused decode step per token
+#define FM_PREFILL_DECODE_MAX_T 8  // up to this many tokens: decode-kernel steps instead of the grouped GEMM
 #define PF_TS 36     // words per row of a wave's transpose buffer: half a 4-bit piece (32 + 4 pad: no bank conflicts)
 
 // One expert's matrices.
@@ -304,6 +304,9 @@ __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageReg
 // stages (np <= 2 pieces, e.g. the down projection's 1024 inputs) the chunk's
 // operands stay resident in LDS and one workgroup walks PF_RL row blocks, the
 // weight ring running on across them; otherwise one row block per workgroup.
+#ifndef PF_WLOAD
+#define PF_WLOAD fm_ldg_u4_nt  // weight pieces: streamed once per chunk
+#endif
 #ifndef PF_RL
 #define PF_RL 8
 #endif
@@ -345,7 +348,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
         const int r0 = rb + 16 * W * rt + 16 * wv;
         const uint32_t w = min((uint32_t)(PW * pc + lw), wpr - 4);
 #pragma unroll
-        for (int j = 0; j < NL; j++) d.c[j] = fm_ldg_u4_nt(mat.w + (size_t)min(r0 + RS * j + lrow, last_row) * wpr + w);
+        for (int j = 0; j < NL; j++) d.c[j] = PF_WLOAD(mat.w + (size_t)min(r0 + RS * j + lrow, last_row) * wpr + w);
         const size_t so = (size_t)min(r0 + n, last_row) * G;  // this lane's fold row
         const uint32_t g0 = PF_GPP * pc;
         if constexpr (VEC) {  // G % PF_GPP == 0: the piece's 8 scales are one 16-byte run
@@ -798,7 +801,12 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
 
 extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool) {
     if (!pool || T <= 0 || K <= 0) return 0;
-    return pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
+    size_t n = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
+    if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K) {  // room for the one-launch decode of a few tokens
+        const size_t d = fm_moe_decode_tokens_workspace_size(T, K, 1, pool->hidden, pool->inter);
+        if (d > n) n = d;
+    }
+    return n;
 }
 
 static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,
@@ -880,11 +888,19 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     PfLayout L = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, has_shared);
     if (!ws || ws_bytes < L.total)
         return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", who, ws_bytes, L.total);
-    // A few tokens (batched decode): one fused decode step per token streams
+    // A few tokens (batched decode): fused decode steps stream
     // each token's experts once at decode efficiency; the grouped GEMM only pays
     // off once experts are shared by many tokens.  Same result per token
     // (batched_prefill.h:241-308 is per-token decode arithmetic).
     if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K) {
+        if (T > 1 && fm_moe_decode_tokens_workspace_size(T, K, has_shared, pool->hidden, pool->inter) <= ws_bytes) {
+            // all tokens in one decode launch when the kernel takes T x (K + shared) slots
+            const int rc = fm_moe_decode_pool_tokens(pool, T, K, idx, weights, shared, shared_bits,
+                                                     shared_gate_scores, X, h_mid, out, out_bf16, ws, ws_bytes,
+                                                     stream);
+            if (rc != FM_ERR_UNSUPPORTED) return rc;
+            fm_clear_error();
+        }
         const size_t dws = fm_moe_decode_workspace_size(K + has_shared, pool->hidden, pool->inter);
         if (dws <= ws_bytes) {
             for (int t = 0; t < T; t++) {
