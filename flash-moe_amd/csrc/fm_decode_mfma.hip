@@ -48,7 +48,7 @@ typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
 #define FM_DX_MARK(n)
 #endif
 
-#define FMM_MAXS 64   // slots of one launch (tokens x slots per token)
+#define FMM_MAXS 136  // slots of one launch: 8 tokens x (16 routed + shared)
 #define FMM_TAB 1024  // pools up to this many experts: the blob/bits tables are staged in LDS
 
 template <int NSLOT>  // slot table entries (the one-pass instance needs few: keeps 3 blocks per CU)
