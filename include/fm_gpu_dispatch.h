@@ -229,7 +229,11 @@ size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool);
  *   out[t] = h_mid[t] + sum_k w[t,k] E_{idx[t,k]}(X[t]) + sigmoid(g[t]) S(X[t])
  * idx/weights: device [T,K]; X, h_mid, out: device [T,hidden] fp32; X values
  * must be bf16-representable (hidden states arrive as bf16); shared,
- * shared_gate_scores (device [T]), h_mid and out_bf16 may be NULL. */
+ * shared_gate_scores (device [T]), h_mid and out_bf16 may be NULL.
+ * Up to 8 tokens (K <= 16, hidden 4096 / inter 1024) run as ONE launch of
+ * the decode kernel over all T x (K + shared) slots (batched decode: few
+ * experts are shared, so grouping buys nothing); bit-equal to
+ * fm_moe_decode_pool per token. */
 int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const int *idx,
                    const float *weights, const fm_expert_weights *shared, int shared_bits,
                    const float *shared_gate_scores, const float *X, const float *h_mid,
