@@ -130,3 +130,41 @@ def test_single_token_17_slots(orc, dev, pool64):
     ref = orc.moe_decode([blobs[e] for e in idx[0]], [bits[e] for e in idx[0]], w[0], x, HIDDEN, INTER,
                          shared_blob=sh_blob, shared_bits=2, shared_score=0.3, h_mid=hm)
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+
+
+@pytest.mark.parametrize("Tn,K,shared_bits,with_hmid", [(3, 8, None, False), (4, 10, 2, True), (7, 6, 4, False)])
+def test_few_tokens_optional_args(orc, dev, pool64, Tn, K, shared_bits, with_hmid):
+    """No shared expert (slots per token = K), a 2-bit shared expert, no h_mid:
+    bit-equal to one fm_moe_decode_pool launch per token, and oracle-checked."""
+    import torch
+    blobs, bits, pool = pool64
+    say("few tokens optional", Tn, K, shared_bits, with_hmid)
+    rng = synth.rng_for(8806, Tn, K)
+    idx, w = orc.route(rng.normal(0, 1, (Tn, 64)).astype(np.float32), K)
+    X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
+    hm = rng.normal(0, 1, (Tn, HIDDEN)).astype(np.float32) if with_hmid else None
+    g = rng.normal(0, 1, Tn).astype(np.float32)
+    sh = sh_blob = dsh = None
+    if shared_bits:
+        sh_blob = synth.expert_blob((8807, shared_bits), HIDDEN, INTER, shared_bits)
+        dsh = T(sh_blob, dev)
+        sh = fm.experts_from_blob(dsh, shared_bits, HIDDEN, INTER)
+    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    fm.workspace_status(ws)
+    out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
+    fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws, shared=sh, shared_bits=shared_bits or 4,
+                   shared_scores=T(g, dev) if sh is not None else None, h_mid=T(hm, dev) if with_hmid else None)
+    torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
+    got = out.cpu().numpy()
+    dws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    o = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    for t in range(Tn):
+        fm.moe_decode_pool(pool, T(idx[t], dev), T(w[t], dev), T(X[t], dev), o, dws, shared=sh,
+                           shared_bits=shared_bits or 4, shared_score=T(g[t:t + 1], dev) if sh is not None else None,
+                           h_mid=T(hm[t], dev) if with_hmid else None)
+        torch.cuda.synchronize()
+        assert np.array_equal(got[t], o.cpu().numpy()), t
+    ref = orc.prefill_moe(idx, w, blobs, bits, X, HIDDEN, INTER, shared_blob=sh_blob, shared_bits=shared_bits or 4,
+                          shared_scores=g if sh is not None else None, h_mid=hm)
+    assert norm_err(got, ref) <= TOL_F32

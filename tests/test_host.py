@@ -128,3 +128,21 @@ def test_workspace_status_rejects_null():
     v = ctypes.c_uint32()
     assert L.fm_workspace_status(None, ctypes.byref(v), None) == -1
     assert b"NULL" in L.fm_last_error()
+
+
+def test_prefill_workspace_covers_few_token_decode():
+    """fm_prefill_moe runs 2-8 tokens (K <= 16) as one decode launch over all
+    T x (K + shared) slots; its workspace query must leave room for that
+    launch's hand-off buffers (status word + per-slot activations and outputs)."""
+    L = fmoe_amd.lib()
+    pool = fmoe_amd.ExpertPool(None, None, 512, 4096, 1024, 64)
+    L.fm_prefill_moe_workspace_size.restype = ctypes.c_size_t
+    L.fm_moe_decode_workspace_size.restype = ctypes.c_size_t
+    for T in range(1, 10):
+        for K in (1, 4, 10, 16):
+            pf = L.fm_prefill_moe_workspace_size(T, K, ctypes.byref(pool))
+            need = L.fm_moe_decode_workspace_size(T * (K + 1), 4096, 1024)
+            # hand-off buffers: 8-byte tagged words per activation and per output row
+            assert need >= T * (K + 1) * (1024 + 4096) * 8
+            if T <= 8:
+                assert pf >= need, (T, K)
