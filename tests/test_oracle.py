@@ -278,3 +278,99 @@ def test_prefill_equals_per_token_decode(orc):
         d = orc.moe_decode([blobs[e] for e in idx[t]], [bits[e] for e in idx[t]], w[t], X[t], H, I,
                            shared_blob=blobs[0], shared_bits=2, shared_score=g[t], h_mid=hm[t])
         assert bits_eq(out[t], d)
+
+
+# ------------------------------------------- dequant GEMM (prefill checker) ---
+@pytest.mark.parametrize("name", ["mv_a", "mv_b", "mv_c"])
+def test_gemm_rows_equal_golden_matvec(orc, name):
+    # shaders.metal:2140-2216 computes, per token column, the matvec of that
+    # token: each output row of the GEMM must be the reference's matvec of its
+    # token, bit for bit.  Token 1 is the golden x itself; the others are
+    # derived tokens checked against the matvec oracle pinned above.
+    g = {k: GOLD[f"{name}_{k}"] for k in "Wsbxy"}
+    x = g["x"]
+    X = np.stack([x[::-1].copy(), x, np.zeros_like(x), (x * 0.5).astype(np.float32)])
+    Y = orc.gemm(4, g["W"], g["s"], g["b"], X)
+    assert bits_eq(Y[1], g["y"])
+    for t in range(X.shape[0]):
+        assert bits_eq(Y[t], orc.matvec(4, g["W"], g["s"], g["b"], X[t]))
+    # the zero token reduces to nothing: every product is (c*s + b) * 0
+    assert np.all(Y[2] == 0.0)
+
+
+def test_gemm_vs_live_reference_and_2bit(orc, ref):
+    rng = synth.rng_for(31)
+    W, s, b = synth.quant_matrix(rng, 24, 1024, 4)
+    X = synth.hidden_vec(rng, 1024, (5, 1024))
+    Y = orc.gemm(4, W, s, b, X)
+    for t in range(5):
+        assert bits_eq(Y[t], ref.matvec4(W, s, b, X[t]))
+    # 2-bit: the same elements widened into nibbles give the same GEMM
+    W2, s2, b2 = synth.quant_matrix(rng, 16, 1024, 2)
+    W4 = orc.pack(4, orc.unpack(2, W2)).reshape(16, 128)
+    assert bits_eq(orc.gemm(2, W2, s2, b2, X), orc.gemm(4, W4, s2, b2, X))
+    for t in range(5):
+        assert bits_eq(orc.gemm(2, W2, s2, b2, X)[t], ref.matvec4(W4, s2, b2, X[t]))
+
+
+# --------------------------------------------------- f32 -> bf16 (RNE) ------
+def _rne_f64(f):
+    """Round-to-nearest-even onto bf16 by exhaustive choice between the two
+    neighbouring bf16 values, distances measured in float64."""
+    u = int(np.float32(f).view(np.uint32))
+    if (u & 0x7F800000) == 0x7F800000:
+        return (u >> 16) | (0x40 if (u & 0x7FFFFF) else 0)
+    lo = u >> 16
+    hi = lo + 1
+    f64 = float(np.float32(f))
+    v_lo = float(np.uint32(lo << 16).view(np.float32))
+    v_hi = float(np.uint32((hi & 0xFFFF) << 16).view(np.float32)) if (hi & 0x7F80) != 0x7F80 or (hi & 0x7F) else None
+    if v_hi is None:  # the next bf16 up is infinity: the value beyond the largest bf16
+        v_hi = np.inf if f64 > 0 else -np.inf
+    d_lo, d_hi = abs(f64 - v_lo), abs(f64 - v_hi)
+    if d_lo < d_hi:
+        return lo
+    if d_hi < d_lo:
+        return hi & 0xFFFF
+    return lo if (lo & 1) == 0 else hi & 0xFFFF
+
+
+def test_f32_to_bf16_rne_cases(orc):
+    f = orc.L.fmo_f32_to_bf16_rne
+    cases = [
+        (1.0, 0x3F80),
+        (-2.0, 0xC000),
+        (0.0, 0x0000),
+        (-0.0, 0x8000),
+        (float(np.uint32(0x3F808000).view(np.float32)), 0x3F80),  # halfway, even below: stays
+        (float(np.uint32(0x3F818000).view(np.float32)), 0x3F82),  # halfway, odd below: rounds up
+        (float(np.uint32(0x3F808001).view(np.float32)), 0x3F81),  # just above halfway
+        (float(np.uint32(0x3F807FFF).view(np.float32)), 0x3F80),  # just below halfway
+        (float(np.uint32(0x3FFF8000).view(np.float32)), 0x4000),  # carry into the exponent
+        (float(np.uint32(0x7F7FFFFF).view(np.float32)), 0x7F80),  # largest float rounds to inf
+        (float("inf"), 0x7F80),
+        (float("-inf"), 0xFF80),
+        (float(np.uint32(0x00008000).view(np.float32)), 0x0000),  # subnormal halfway, even
+        (float(np.uint32(0x00018000).view(np.float32)), 0x0002),  # subnormal halfway, odd
+    ]
+    for x, want in cases:
+        assert f(x) == want, (hex(int(np.float32(x).view(np.uint32))), hex(f(x)), hex(want))
+    # NaN stays NaN (quiet), sign kept
+    for nan_bits in (0x7FC00000, 0x7F800001, 0xFF800001, 0x7F810000):
+        r = f(float(np.uint32(nan_bits).view(np.float32)))
+        assert (r & 0x7F80) == 0x7F80 and (r & 0x7F) != 0 and (r >> 15) == (nan_bits >> 31)
+
+
+def test_f32_to_bf16_rne_vs_float64_brute(orc):
+    rng = np.random.default_rng(5)
+    u = rng.integers(0, 2**32, 20000, dtype=np.uint64).astype(np.uint32)
+    u = u[(u & 0x7F800000) != 0x7F800000]
+    # plus every low-half pattern near the rounding boundary of one value
+    u = np.concatenate([u, 0x40490000 + np.arange(0x7F00, 0x8100, dtype=np.uint32),
+                        0x40480000 + np.arange(0x7F00, 0x8100, dtype=np.uint32)])
+    for v in u.view(np.float32):
+        assert orc.L.fmo_f32_to_bf16_rne(float(v)) == _rne_f64(v), hex(int(np.float32(v).view(np.uint32)))
+    # agrees with truncation whenever the dropped half is below halfway
+    low = u[(u & 0xFFFF) < 0x8000]
+    for v in low[:2000].view(np.float32):
+        assert orc.L.fmo_f32_to_bf16_rne(float(v)) == orc.L.fmo_f32_to_bf16_trunc(float(v))
