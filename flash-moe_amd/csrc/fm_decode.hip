@@ -374,8 +374,8 @@ __device__ __forceinline__ void fm_dot_gu(const FmUnitW &g, const FmUnitW &u, co
             u0 = fm_dot_word2(uw[p], q, u0);
         }
     }
-    pg = __builtin_fmaf(g.s * 16777216.0f, g0 + g1, g.b * x.sum);
-    pu = __builtin_fmaf(u.s * 16777216.0f, u0 + u1, u.b * x.sum);
+    pg = __builtin_fmaf(g.s * x.inv, g0 + g1, g.b * x.sum);
+    pu = __builtin_fmaf(u.s * x.inv, u0 + u1, u.b * x.sum);
 }
 
 // one group dot with four accumulator chains
@@ -400,7 +400,7 @@ __device__ __forceinline__ float fm_dot_one(const FmUnitW &g, const FmXGroup &x)
         c2 = fm_dot_word2(gw[2], &x.q[16], c2);
         c3 = fm_dot_word2(gw[3], &x.q[24], c3);
     }
-    return __builtin_fmaf(g.s * 16777216.0f, (c0 + c1) + (c2 + c3), g.b * x.sum);
+    return __builtin_fmaf(g.s * x.inv, (c0 + c1) + (c2 + c3), g.b * x.sum);
 }
 
 template <int LH, int LI>

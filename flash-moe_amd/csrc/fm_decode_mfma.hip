@@ -57,7 +57,9 @@ struct __attribute__((aligned(16))) FmmLds {
     fm_h2 aq[2][FMM_GI][32];  // the B slot's activations, same layouts
     fm_h2 zero[32];           // zero operand rows (128 B)
     float xsum[FMM_GH];       // per-group sums of x
+    float xinv[FMM_GH];       // per-group 2^(24 - e): x operands carry x * 2^e
     float asum[FMM_GI];       // per-group sums of the activations
+    float ainv[FMM_GI];       // per-group 2^(24 - e) of the activation operands
     union {
         float act[FMM_MAXI];            // staged activations (fp32)
         const char *tab[FMM_TAB / 2];   // prologue: pool blob table, first half
@@ -128,18 +130,18 @@ FM_DEV fmm_h8 fmm_codes(uint32_t w, int h) {
 
 FM_DEV fmm_h8 fmm_lds_op(const fm_h2 *p) { return __builtin_bit_cast(fmm_h8, *(const fm_u4 *)p); }
 
-// One 64-element group of v (fp32, in LDS) -> operand row layout for BITS,
-// 32 pairs; thread e (0..31) writes pair e.
-FM_DEV void fmm_build_pair(const float *v, int bits, int e, fm_h2 *dst) {
+// One 64-element group of v (fp32, in LDS), scaled by f = 2^e -> operand row
+// layout for BITS, 32 pairs; this call writes pair e.
+FM_DEV void fmm_build_pair(const float *v, int bits, int e, float f, fm_h2 *dst) {
     if (bits == 4) {
         const int p = e >> 2, j = e & 3;
-        const float m = (j & 1) ? 0.0625f : 1.f;
+        const float m = (j & 1) ? 0.0625f * f : f;
         dst[e] = fm_pack_h2(v[8 * p + j] * m, v[8 * p + 4 + j] * m);
     } else {
         const int p = e >> 3, n = e & 7;
         // pair n: (x_n, x_{n+8}) / 4^(field position of code n in the word)
         const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
-        dst[e] = fm_pack_h2(v[16 * p + n] * mt[n], v[16 * p + 8 + n] * mt[n]);
+        dst[e] = fm_pack_h2(v[16 * p + n] * (mt[n] * f), v[16 * p + 8 + n] * (mt[n] * f));
     }
 }
 
@@ -271,17 +273,18 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
     }
 }
 
-// Fold: lane (row n, q) holds D[4q+v][n] = dot of row n with group g0+4q+v.
-FM_DEV float fmm_fold(const fmm_f4 &d, fmm_u2 sc, fmm_u2 bi, const float *gsum4) {
+// Fold: lane (row n, q) holds D[4q+v][n] = dot of row n with group g0+4q+v;
+// ginv4 undoes each group's operand scale (and the codes' 2^-24).
+FM_DEV float fmm_fold(const fmm_f4 &d, fmm_u2 sc, fmm_u2 bi, const float *gsum4, const float *ginv4) {
     const float s0 = __uint_as_float(sc.x << 16), s1 = __uint_as_float(sc.x & 0xffff0000u);
     const float s2 = __uint_as_float(sc.y << 16), s3 = __uint_as_float(sc.y & 0xffff0000u);
     const float b0 = __uint_as_float(bi.x << 16), b1 = __uint_as_float(bi.x & 0xffff0000u);
     const float b2 = __uint_as_float(bi.y << 16), b3 = __uint_as_float(bi.y & 0xffff0000u);
-    const float K24 = 16777216.0f;
-    float r = __builtin_fmaf(s0 * K24, d[0], b0 * gsum4[0]);
-    r += __builtin_fmaf(s1 * K24, d[1], b1 * gsum4[1]);
-    r += __builtin_fmaf(s2 * K24, d[2], b2 * gsum4[2]);
-    r += __builtin_fmaf(s3 * K24, d[3], b3 * gsum4[3]);
+    const fm_f4 gi = *(const fm_f4 *)ginv4, gs = *(const fm_f4 *)gsum4;
+    float r = __builtin_fmaf(s0 * gi.x, d[0], b0 * gs.x);
+    r += __builtin_fmaf(s1 * gi.y, d[1], b1 * gs.y);
+    r += __builtin_fmaf(s2 * gi.z, d[2], b2 * gs.z);
+    r += __builtin_fmaf(s3 * gi.w, d[3], b3 * gs.w);
     return r;
 }
 
@@ -424,24 +427,35 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             v[4 * j + 2] = xr[j].z;
             v[4 * j + 3] = xr[j].w;
         }
+        // the group's operand scale 2^e (its 4 threads are adjacent lanes)
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
         // 4-bit words 2qq, 2qq+1: pair j of word p = (x_{8p+j}, x_{8p+4+j}) * (j odd ? 1/16 : 1)
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float m = (j & 1) ? 0.0625f : 1.f;
+                const float m = (j & 1) ? 0.0625f * f : f;
                 L.xq[0][g][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
             }
         // 2-bit word qq: pair n = (x_n, x_{n+8}) / 4^(field position of code n)
         const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
 #pragma unroll
-        for (int n = 0; n < 8; n++) L.xq[1][g][8 * qq + n] = fm_pack_h2(v[n] * mt[n], v[8 + n] * mt[n]);
+        for (int n = 0; n < 8; n++) L.xq[1][g][8 * qq + n] = fm_pack_h2(v[n] * (mt[n] * f), v[8 + n] * (mt[n] * f));
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
-        if (qq == 0) L.xsum[g] = s;
+        if (qq == 0) {
+            L.xsum[g] = s;
+            L.xinv[g] = fm_exp2i(24 - ex);
+        }
     }
     __syncthreads();
 
@@ -457,9 +471,9 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
             fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         }
-        const float *gs4 = &L.xsum[16 * wv + 4 * q];
-        float pg = fmm_fold(g0 + g1, sg, bg, gs4);
-        float pu = fmm_fold(u0 + u1, su, bu, gs4);
+        const float *gs4 = &L.xsum[16 * wv + 4 * q], *gi4 = &L.xinv[16 * wv + 4 * q];
+        float pg = fmm_fold(g0 + g1, sg, bg, gs4, gi4);
+        float pu = fmm_fold(u0 + u1, su, bu, gs4, gi4);
         pg = fmm_q_sum(pg);
         pu = fmm_q_sum(pu);
         if (lane < 16) {
@@ -513,15 +527,24 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     }
     __syncthreads();
     if (doB) {
-        // per-group sums (16 threads x 4 elements per group) and operand rows
+        // per group (16 threads x 4 elements): sum, operand scale 2^e, and the
+        // operand rows (2 pairs per thread)
+        const int lay = sB.bits == 4 ? 0 : 1;
         for (uint32_t g = tid >> 4; g < GI; g += 16) {
             const float *ag = L.act + 64 * g + 4 * (tid & 15);
             float s = (ag[0] + ag[1]) + (ag[2] + ag[3]);
+            float mx = fmaxf(fmaxf(fabsf(ag[0]), fabsf(ag[1])), fmaxf(fabsf(ag[2]), fabsf(ag[3])));
             s = fmm_row_sum(s);
-            if ((tid & 15) == 0) L.asum[g] = s;
+            mx = fm_row16_max(mx);
+            const int ex = fm_group_shift(mx);
+            const float f = fm_exp2i(ex);
+            if ((tid & 15) == 0) {
+                L.asum[g] = s;
+                L.ainv[g] = fm_exp2i(24 - ex);
+            }
+            fmm_build_pair(L.act + 64 * g, sB.bits, 2 * (tid & 15), f, &L.aq[lay][g][0]);
+            fmm_build_pair(L.act + 64 * g, sB.bits, 2 * (tid & 15) + 1, f, &L.aq[lay][g][0]);
         }
-        const int lay = sB.bits == 4 ? 0 : 1;
-        for (uint32_t e = tid; e < GI * 32; e += 256) fmm_build_pair(L.act + 64 * (e >> 5), sB.bits, e & 31, &L.aq[lay][e >> 5][0]);
     }
     __syncthreads();
     FM_DX_MARK(5);
@@ -533,7 +556,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             fmm_mma<4>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         else
             fmm_mma<2>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
-        float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q]);
+        float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q], &L.ainv[4 * q]);
         y = fmm_q_sum(y);
         const uint32_t row = rowB0 + n;
         if (lane < 16) {

@@ -12,6 +12,15 @@
 // Per 4-bit word (8 codes): one shift, four ANDs, four dot2 = 1.1 VALU ops per
 // code, which keeps an HBM-rate stream under the CU's vector issue budget.
 // (fp16 denormals are preserved: the kernels run with denorm mode 16/64 = 3.)
+//
+// Operand range.  x enters the dot products as fp16, so every 64-element group
+// is first scaled by a power of two 2^e chosen from the group's largest |x|
+// (fm_group_shift: max |x| * 2^e lands in [2^14, 2^15)).  The field factors
+// (down to 2^-8 for 2-bit fields) then still leave every value of the group
+// inside fp16's normal range, whatever the magnitude of x (1e-6 or 3e4): the
+// fp16 rounding error is at most 2^-12 of the group's largest |x|.  The
+// inverse 2^(24-e) -- with the 2^24 of the subnormal codes -- multiplies the
+// group scale in the fold; the group sum stays unscaled fp32.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -53,25 +62,48 @@ FM_DEV float fm_dot2(fm_h2 a, fm_h2 b, float c) { return __builtin_amdgcn_fdot2(
 struct FmXGroup {
     fm_h2 q[32];
     float sum;
+    float inv;  // 2^(24 - e): the group's operand scale 2^e undone, codes' 2^-24 folded in
 };
+
+// 2^e as a float, e in [-126, 127] (exact).
+FM_DEV float fm_exp2i(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// Shift e for a group whose largest magnitude is amax: amax * 2^e in [2^14, 2^15)
+// (clamped to [-100, 100]: all-zero or subnormal groups take 2^100, which keeps
+// 2^(24 - e) a normal float).
+FM_DEV int fm_group_shift(float amax) {
+    const int E = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127;
+    return min(max(14 - E, -100), 100);
+}
 
 template <int BITS>
 FM_DEV void fm_load_xgroup(const float *__restrict__ xg, FmXGroup &g) {
-    float s = 0.f;
+    float s = 0.f, mx = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; p++) {
+        const fm_f4 a = *(const fm_f4 *)(xg + 4 * p);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+    const int e = fm_group_shift(mx);
+    const float f = fm_exp2i(e);
+    g.inv = fm_exp2i(24 - e);
     if constexpr (BITS == 4) {
+        const float f16 = f * 0.0625f;
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             fm_f4 a = *(const fm_f4 *)(xg + 8 * p);
             fm_f4 b = *(const fm_f4 *)(xg + 8 * p + 4);
-            g.q[4 * p + 0] = fm_pack_h2(a.x, b.x);
-            g.q[4 * p + 1] = fm_pack_h2(a.y * 0.0625f, b.y * 0.0625f);
-            g.q[4 * p + 2] = fm_pack_h2(a.z, b.z);
-            g.q[4 * p + 3] = fm_pack_h2(a.w * 0.0625f, b.w * 0.0625f);
+            g.q[4 * p + 0] = fm_pack_h2(a.x * f, b.x * f);
+            g.q[4 * p + 1] = fm_pack_h2(a.y * f16, b.y * f16);
+            g.q[4 * p + 2] = fm_pack_h2(a.z * f, b.z * f);
+            g.q[4 * p + 3] = fm_pack_h2(a.w * f16, b.w * f16);
             s += ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
         }
     } else {
         // code field n of a 2-bit word sits at bit 2n (n <= 4) or 2(n-5) after >> 10
-        const float m[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+        float m[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+        for (int i = 0; i < 8; i++) m[i] *= f;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             fm_f4 a0 = *(const fm_f4 *)(xg + 16 * p);
@@ -158,7 +190,7 @@ FM_DEV float fm_group_dot(const FmWGroup &w, const FmXGroup &x, float s, float b
         acc0 = fm_dot_word2(w.a.z, &x.q[16], acc0);
         acc1 = fm_dot_word2(w.a.w, &x.q[24], acc1);
     }
-    return __builtin_fmaf(s * 16777216.0f, acc0 + acc1, b * x.sum);  // codes carried * 2^-24
+    return __builtin_fmaf(s * x.inv, acc0 + acc1, b * x.sum);  // codes carried * 2^-24, x * 2^e
 }
 
 // DPP lane moves (GFX9 encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
@@ -188,6 +220,15 @@ FM_DEV float fm_lane_sum(float v) {
         const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
         v = (v + r1) + (r2 + r3);
     }
+    return v;
+}
+
+// Max over each aligned 16-lane DPP row (valid in every lane of the row).
+FM_DEV float fm_row16_max(float v) {
+    v = fmaxf(v, fm_dpp_f<0xB1>(v));
+    v = fmaxf(v, fm_dpp_f<0x4E>(v));
+    v = fmaxf(v, fm_dpp_f<0x124>(v));
+    v = fmaxf(v, fm_dpp_f<0x128>(v));
     return v;
 }
 

@@ -19,9 +19,12 @@
 // fp16 subnormals exactly.  Each 64-element group accumulates in its own fp32
 // MFMA tile, then folds  acc += s_g * 2^24 * D_g + b_g * sum(x_g)  in fp32, as
 // the reference's per-group affine dequant requires.  Token inputs enter as
-// fp16 (bf16-exact hidden states; activations round like the decode path's)
-// pre-scaled to match the code field positions; plain fm_pfb_gemm adds an fp16
-// residual term for arbitrary fp32 inputs.  Group sums come from fp32.
+// fp16, scaled by one power of two per token row (largest |x| of the row
+// lands in [2^14, 2^15), so no value overflows fp16 and small rows keep their
+// precision), times the code field factors; plain fm_pfb_gemm adds an fp16
+// residual term so fp32 inputs keep ~22 bits.  The row's scale is undone once,
+// on the accumulated row; group sums are fp32, pre-multiplied by the same
+// scale so the fold stays  acc += s_g * D_g + b_g * sum'(x_g).
 //
 // MFMA 16x16x32 operand layouts (gfx950): lane l holds A[l%16][8*(l/16)+0..7],
 // B[8*(l/16)+0..7][l%16], and D[4*(l/16)+v][l%16] for v = 0..3.  Here A = 16
@@ -70,7 +73,8 @@ struct PfArgs {
     // 2-bit [1] pair layouts (lo: residual terms, mode 2 only) + group sums.
     // Source row: mode 0 token, mode 1 entry position, mode 2 token.
     const fm_h2 *xop[2], *xlo[2];
-    const float *xsum;
+    const float *xsum;  // group sums times the row's 2^(e - 24)
+    const float *xinv;  // per source row: 2^(24 - e), applied to the finished accumulators
     uint32_t in_dim, out_dim;
     // outputs
     float *gout, *uout;  // mode 0: [entries][inter]
@@ -138,76 +142,95 @@ __device__ __forceinline__ fm_h8 pf_codes(uint32_t w, int h) {
 }
 
 // ---------------------------------------------------------------- operands -
-// One 64-element group of a source row -> its B-operand pairs in both code
-// layouts (4-bit words: (x_j, x_{j+4}) * (j odd ? 2^-4 : 1); 2-bit words:
-// (x_n, x_{n+8}) / 4^(field of n)), optional residual terms, and the group
-// sum.  Four threads per group, 16 elements each.
+// One source row per workgroup -> its B-operand pairs in both code layouts
+// (4-bit words: (x_j, x_{j+4}) * (j odd ? 2^-4 : 1); 2-bit words:
+// (x_n, x_{n+8}) / 4^(field of n)), all times the row's 2^e, optional residual
+// terms, the group sums times 2^(e - 24) and the row's 2^(24 - e).  A thread
+// takes 16 consecutive elements (a quarter group) per step: one pass for the
+// row's largest |x|, one to convert.
+__device__ __forceinline__ void pf_xop_load16(const float *src, const float *src2, size_t o, float (&v)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const fm_f4 t = fm_ldg_f4(src + o + 4 * j);
+        v[4 * j] = t.x;
+        v[4 * j + 1] = t.y;
+        v[4 * j + 2] = t.z;
+        v[4 * j + 3] = t.w;
+    }
+    if (src2) {  // SwiGLU of separately computed gate and up rows
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const fm_f4 t = fm_ldg_f4(src2 + o + 4 * j);
+            v[4 * j] = fm_silu_mul(v[4 * j], t.x);
+            v[4 * j + 1] = fm_silu_mul(v[4 * j + 1], t.y);
+            v[4 * j + 2] = fm_silu_mul(v[4 * j + 2], t.z);
+            v[4 * j + 3] = fm_silu_mul(v[4 * j + 3], t.w);
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict__ src, const float *__restrict__ src2,
                                                         const int *__restrict__ nrows_dev, int nrows_max,
                                                         uint32_t in_dim, fm_h2 *x4, fm_h2 *x2, fm_h2 *l4, fm_h2 *l2,
-                                                        float *xsum) {
-    const uint32_t G = in_dim / 64;
-    const uint32_t q = blockIdx.x * 256 + threadIdx.x;  // (row, group, quarter)
+                                                        float *xsum, float *xinv) {
+    __shared__ float wmax[4];
+    const uint32_t G = in_dim / 64, nq = in_dim / 16;
+    const uint32_t row = blockIdx.x;
     const int nrows = nrows_dev ? *nrows_dev : nrows_max;
-    const uint32_t row = q / (4 * G), g = (q / 4) % G, qq = q & 3;
-    const bool live = row < (uint32_t)nrows;
+    if (row >= (uint32_t)nrows) return;
+    const int tid = threadIdx.x;
+    const size_t rbase = (size_t)row * in_dim;
     float v[16];
-    if (live) {
-        const float *xp = src + (size_t)row * in_dim + 64 * g + 16 * qq;
+    float mx = 0.f;
+    for (uint32_t qi = tid; qi < nq; qi += 256) {
+        pf_xop_load16(src, src2, rbase + 16 * qi, v);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const fm_f4 t = fm_ldg_f4(xp + 4 * j);
-            v[4 * j] = t.x;
-            v[4 * j + 1] = t.y;
-            v[4 * j + 2] = t.z;
-            v[4 * j + 3] = t.w;
-        }
-        if (src2) {  // SwiGLU of separately computed gate and up rows
-            const float *up = src2 + (size_t)row * in_dim + 64 * g + 16 * qq;
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+    }
+    mx = fmaxf(mx, fm_row16_max(mx));
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16)));
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)));
+    mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48)));
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const int ex = fm_group_shift(mx);
+    const float f = fm_exp2i(ex), fs = fm_exp2i(ex - 24);
+    if (tid == 0) xinv[row] = fm_exp2i(24 - ex);
+    float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+    for (int n = 0; n < 8; n++) mt[n] *= f;
+    for (uint32_t qi = tid; qi < nq; qi += 256) {
+        const uint32_t g = qi / 4, qq = qi & 3;
+        pf_xop_load16(src, src2, rbase + 16 * qi, v);
+        const size_t base = ((size_t)row * G + g) * 32;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const fm_f4 t = fm_ldg_f4(up + 4 * j);
-                v[4 * j] = fm_silu_mul(v[4 * j], t.x);
-                v[4 * j + 1] = fm_silu_mul(v[4 * j + 1], t.y);
-                v[4 * j + 2] = fm_silu_mul(v[4 * j + 2], t.z);
-                v[4 * j + 3] = fm_silu_mul(v[4 * j + 3], t.w);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = 0.f;
-    }
-    const size_t base = ((size_t)row * G + g) * 32;
-    const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float m = (j & 1) ? 0.0625f : 1.f;
-            const float a = v[8 * h + j] * m, b = v[8 * h + 4 + j] * m;
-            const fm_h2 hi = fm_pack_h2(a, b);
-            const size_t o = base + 4 * (2 * qq + h) + j;
-            if (live) {
+                const float m = (j & 1) ? 0.0625f * f : f;
+                const float a = v[8 * h + j] * m, b = v[8 * h + 4 + j] * m;
+                const fm_h2 hi = fm_pack_h2(a, b);
+                const size_t o = base + 4 * (2 * qq + h) + j;
                 x4[o] = hi;
                 if (l4) l4[o] = fm_pack_h2(a - (float)hi.x, b - (float)hi.y);
             }
-        }
 #pragma unroll
-    for (int n = 0; n < 8; n++) {
-        const float a = v[n] * mt[n], b = v[8 + n] * mt[n];
-        const fm_h2 hi = fm_pack_h2(a, b);
-        const size_t o = base + 8 * qq + n;
-        if (live) {
+        for (int n = 0; n < 8; n++) {
+            const float a = v[n] * mt[n], b = v[8 + n] * mt[n];
+            const fm_h2 hi = fm_pack_h2(a, b);
+            const size_t o = base + 8 * qq + n;
             x2[o] = hi;
             if (l2) l2[o] = fm_pack_h2(a - (float)hi.x, b - (float)hi.y);
         }
-    }
-    float s = 0.f;
+        float sm = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) s += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if (live && qq == 0) xsum[(size_t)row * G + g] = s;
+        for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+        // the 4 quarters of a group are adjacent lanes (qi = tid + 256 k, 256 % 4 == 0)
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if (qq == 0) xsum[(size_t)row * G + g] = sm * fs;
+    }
 }
 
 // ---------------------------------------------------------------- gemm -----
@@ -404,7 +427,7 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, c1, d, 0, 0, 0);
             }
             const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
-            const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1)))) * 16777216.0f;
+            const float sc = fm_bf16_to_f32((uint16_t)(sw[gg >> 1] >> (16 * (gg & 1))));
             const float bi = fm_bf16_to_f32((uint16_t)(bw[gg >> 1] >> (16 * (gg & 1))));
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(sc, d[v], __builtin_fmaf(bi, xs[v], acc[v]));
@@ -509,6 +532,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
     __shared__ PfStage<LO> st[NST];
     __shared__ uint32_t tbuf[W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
+    __shared__ float tinv_s[PF_TOK];  // each token column's 2^(24 - e)
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     // Units are (chunk, matrix, row block) over the LIVE chunks only (the grid is
     // sized for max_chunks; surplus blocks exit).  XCD-aware order: the 8 XCDs
@@ -554,6 +578,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
         const int sr = sl < 0 ? -1 : (a.mode == 1 ? off + ei : (a.mode == 2 ? sl : pf_token_of_slot(a, sl)));
         slot_s[ei] = sl;
         srow_s[ei] = sr;
+        tinv_s[ei] = sr < 0 ? 0.f : a.xinv[sr];
     }
     __syncthreads();
     int bits = 4;
@@ -570,12 +595,13 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
         for (int v = 0; v < 4; v++) {
             const int tk = 4 * q + v;
             if (tk >= n) continue;
+            const float ti = tinv_s[tk];
             if constexpr (DUAL) {  // SwiGLU in the epilogue: gout receives the activation
-                a.gout[(size_t)(off + tk) * a.out_dim + row] = fm_silu_mul(acc[v], acc2[v]);
+                a.gout[(size_t)(off + tk) * a.out_dim + row] = fm_silu_mul(acc[v] * ti, acc2[v] * ti);
             } else if (a.mode == 0) {
-                (mat == 0 ? a.gout : a.uout)[(size_t)(off + tk) * a.out_dim + row] = acc[v];
+                (mat == 0 ? a.gout : a.uout)[(size_t)(off + tk) * a.out_dim + row] = acc[v] * ti;
             } else {
-                a.y[(size_t)slot_s[tk] * a.out_dim + row] = acc[v];
+                a.y[(size_t)slot_s[tk] * a.out_dim + row] = acc[v] * ti;
             }
         }
     };
@@ -747,7 +773,7 @@ static uint32_t pf_max_chunks(int T, int K, uint32_t E, int has_shared) {
 // B-operand block for `rows` source rows of in_dim inputs: pairs in both code
 // layouts (+ residual terms when lo), group sums.
 struct PfOps {
-    size_t x4, x2, l4, l2, sum, total;
+    size_t x4, x2, l4, l2, sum, inv, total;
 };
 
 static PfOps pf_ops_layout(size_t rows, uint32_t in_dim, bool lo, size_t o) {
@@ -763,6 +789,8 @@ static PfOps pf_ops_layout(size_t rows, uint32_t in_dim, bool lo, size_t o) {
     if (lo) o += fm_align_up(pairs, 256);
     P.sum = o;
     o += fm_align_up(rows * (in_dim / 64) * sizeof(float), 256);
+    P.inv = o;
+    o += fm_align_up(rows * sizeof(float), 256);
     P.total = o;
     return P;
 }
@@ -811,11 +839,10 @@ extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_po
 
 static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,
                          char *base, const PfOps &P, bool lo, hipStream_t st) {
-    const size_t threads = (size_t)nrows_max * (in_dim / 64) * 4;
-    hipLaunchKernelGGL(fm_pf_xop_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, src2, nrows_dev,
+    hipLaunchKernelGGL(fm_pf_xop_kernel, dim3((unsigned)nrows_max), dim3(256), 0, st, src, src2, nrows_dev,
                        nrows_max, in_dim, (fm_h2 *)(base + P.x4), (fm_h2 *)(base + P.x2),
                        lo ? (fm_h2 *)(base + P.l4) : nullptr, lo ? (fm_h2 *)(base + P.l2) : nullptr,
-                       (float *)(base + P.sum));
+                       (float *)(base + P.sum), (float *)(base + P.inv));
     return fm_check_launch("fm_pf_xop_kernel");
 }
 
@@ -825,6 +852,7 @@ static void pf_bind_ops(PfArgs &a, char *base, const PfOps &P, bool lo) {
     a.xlo[0] = lo ? (const fm_h2 *)(base + P.l4) : nullptr;
     a.xlo[1] = lo ? (const fm_h2 *)(base + P.l2) : nullptr;
     a.xsum = (const float *)(base + P.sum);
+    a.xinv = (const float *)(base + P.inv);
 }
 
 // Gate and up rows in one workgroup with the whole input resident (eight
@@ -931,7 +959,7 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
                        (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err));
     int rc = fm_check_launch("fm_pf_lists_kernel");
     if (rc) return rc;
-    // token operands of X (hidden states are bf16-exact: fp16 hi only)
+    // token operands of X (fp16, one power-of-two scale per token)
     rc = pf_launch_ops(X, nullptr, nullptr, T, pool->hidden, p, L.xo, false, st);
     if (rc) return rc;
 

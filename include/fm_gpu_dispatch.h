@@ -227,8 +227,9 @@ size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool);
  * Same result as the per-token loop of batched_prefill.h:241-308 plus the
  * shared expert of pfb_batched_shared_expert (batched_prefill.h:122-226):
  *   out[t] = h_mid[t] + sum_k w[t,k] E_{idx[t,k]}(X[t]) + sigmoid(g[t]) S(X[t])
- * idx/weights: device [T,K]; X, h_mid, out: device [T,hidden] fp32; X values
- * must be bf16-representable (hidden states arrive as bf16); shared,
+ * idx/weights: device [T,K]; X, h_mid, out: device [T,hidden] fp32 (X enters
+ * the matrix cores as fp16 scaled by a power of two per token, so any finite
+ * magnitude keeps ~11 bits relative to the token's largest |x|); shared,
  * shared_gate_scores (device [T]), h_mid and out_bf16 may be NULL.
  * Up to 8 tokens (K <= 16, hidden 4096 / inter 1024) run as ONE launch of
  * the decode kernel over all T x (K + shared) slots (batched decode: few

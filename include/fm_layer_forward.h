@@ -52,7 +52,7 @@ size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T);
 /* Prefill of T tokens: the MoE part of batched_prefill (batched_prefill.h:
  * 122-308) -- router and shared-expert-gate GEMMs over all tokens, per-token
  * routing, then the grouped expert GEMM (routed + shared) and the combine.
- * h_post, h_mid, out: device [T, hidden] fp32, h_post bf16-representable. */
+ * h_post, h_mid, out: device [T, hidden] fp32. */
 int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
                            const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
                            size_t ws_bytes, void *stream);
