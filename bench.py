@@ -76,7 +76,7 @@ def bench_decode(args, dev):
     hm = torch.from_numpy(rng.normal(0, 1, H).astype(np.float32)).to(dev)
     idx = torch.empty((nsteps, K), dtype=torch.int32, device=dev)
     w = torch.empty((nsteps, K), dtype=torch.float32, device=dev)
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, H, I), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, H, I), dev)
     out = torch.empty(H, dtype=torch.float32, device=dev)
     ob = torch.empty(H, dtype=torch.int16, device=dev)
 
@@ -135,7 +135,7 @@ def bench_decode(args, dev):
     Lr.shared_bits = 4
     Lr.has_shared = 1
     Lr.pool = pool.c
-    lws = torch.zeros(fm.moe_forward_workspace_bytes(Lr, K), dtype=torch.uint8, device=dev)
+    lws = fm.workspace(fm.moe_forward_workspace_bytes(Lr, K), dev)
     hps = torch.from_numpy(synth.hidden_vec(rng, H, (16, H))).to(dev)
     for i in range(args.warmup):
         Lr.shared = shared[i % n_sh]
@@ -185,7 +185,7 @@ def bench_prefill(args, dev, pool):
     sh = fm.experts_from_blob(sh_blob, 4, H, I)
     idx = torch.empty((Tn, K), dtype=torch.int32, device=dev)
     w = torch.empty((Tn, K), dtype=torch.float32, device=dev)
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     out = torch.empty((Tn, H), dtype=torch.float32, device=dev)
     ob = torch.empty((Tn, H), dtype=torch.int16, device=dev)
 
@@ -245,9 +245,9 @@ def bench_tiered(args, dev):
         out = torch.empty((B, H), dtype=torch.float32, device=dev)
         ob = torch.empty((B, H), dtype=torch.int16, device=dev)
         if B == 1:
-            ws = torch.zeros(fm.decode_workspace_bytes(K + 1, H, I), dtype=torch.uint8, device=dev)
+            ws = fm.workspace(fm.decode_workspace_bytes(K + 1, H, I), dev)
         else:
-            ws = torch.empty(fm.prefill_workspace_bytes(B, K, pool), dtype=torch.uint8, device=dev)
+            ws = fm.workspace(fm.prefill_workspace_bytes(B, K, pool), dev)
 
         def step(i):
             fm.route_topk(logits[i], K, idx[i], w[i])
@@ -323,7 +323,7 @@ def bench_small(args, dev, pool):
     torch.cuda.synchronize()
     mv_us = e0.elapsed_time(e1) * 1e3 / steps
     mv_bytes = 4096 * 512 * 4 + 2 * 4096 * 64 * 2 + 4096 * 2 + 4096 * 4
-    ws = torch.zeros(fm.decode_workspace_bytes(1, H, I), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(1, H, I), dev)
     out = torch.empty(H, dtype=torch.float32, device=dev)
     ex_args = []
     for e in range(E):

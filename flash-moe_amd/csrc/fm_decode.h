@@ -41,9 +41,9 @@ struct FmDecodeArgs {
     float *expert_out;
     uint64_t *act2;  // [S][inter]  (value bits | epoch << 32) SwiGLU activations
     uint64_t *y2;    // [S][hidden] (value bits | epoch << 32) per-slot down outputs
-    uint32_t *err;   // set when a bounded wait gave up
-    uint32_t epoch;  // this call's tag (never 0)
-    int phases;      // mfma kernel: bit 0 gate/up, bit 1 down+combine (0 = both)
+    uint32_t *err;      // workspace status word (FM_STATUS_* bits)
+    uint32_t *ws_epoch; // workspace header: tag of the last completed call
+    uint32_t *ws_done;  // workspace header: counted units of the running call that finished
     // optional next-layer input RMS norm of out (cpu_kernels.h:235-246)
     const uint16_t *norm_w;  // bf16 [hidden] or NULL
     float norm_eps;
@@ -86,7 +86,21 @@ __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k, int 
 // consumer polls the 64-bit words it needs with agent-coherent loads until
 // every tag equals the epoch.  No counters (which would serialise thousands of
 // device-scope atomics on one cache line), no L2 write-back/invalidate, and no
-// reset: a new call simply uses a new epoch.
+// reset between calls.
+//
+// The epoch lives in the workspace header, on the device, so a call recorded
+// into a graph tags each replay differently:
+//   +0   status word (FM_STATUS_* bits, fm_workspace_status)
+//   +64  epoch of the last completed call (0 after fm_workspace_init)
+//   +128 count of the running call's finished units
+// Every workgroup reads the header epoch once before its first barrier and
+// tags with epoch + 1; the workgroups (or work items) that end the hand-off
+// chains -- the combining ones -- bump the count after their last tagged
+// access, and the last one stores the new epoch and clears the count.  Tags
+// only grow, and the tagged region is written only with tags, so after
+// fm_workspace_init (all zero) a stale word never carries the running call's
+// tag.  (After 2^32 - 1 calls the tag wraps: the status word then reports
+// FM_STATUS_EPOCH_WRAP and the workspace needs fm_workspace_init again.)
 __device__ __forceinline__ void fm_put_tagged(uint64_t *p, float v, uint32_t epoch) {
     __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -94,6 +108,27 @@ __device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 #define FM_SPIN_MAX (1u << 16)
+#define FM_WS_EPOCH_OFF 64
+#define FM_WS_DONE_OFF 128
+
+// This call's tag (one thread per workgroup, before the workgroup's first barrier).
+__device__ __forceinline__ uint32_t fm_epoch_read(const FmDecodeArgs &a) {
+    const uint32_t e = __hip_atomic_load(a.ws_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    return e ? e : 1u;
+}
+
+// One thread per counted unit of work, after its last tagged access: the last
+// of `total` units publishes the epoch for the next call.  Counted units must
+// be the ends of every hand-off chain (every workgroup that reads the epoch and
+// tags a word feeds, directly or not, one of them), so when the last one
+// arrives every tag user of this call has read the epoch.
+__device__ __forceinline__ void fm_epoch_finish(const FmDecodeArgs &a, uint32_t ep, uint32_t total) {
+    if (atomicAdd(a.ws_done, 1u) == total - 1) {
+        __hip_atomic_store(a.ws_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.ws_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ep == 0xFFFFFFFFu) atomicOr(a.err, FM_STATUS_EPOCH_WRAP);
+    }
+}
 
 // Alternative launchers tried by fm_decode_launch before the eager kernel;
 // each returns FM_ERR_UNSUPPORTED (message cleared by the caller) when the

@@ -22,7 +22,6 @@
 // resolved on the device from routing indices (no host round trip).
 #include "fm_decode.h"
 
-#include <atomic>
 #include <stdlib.h>
 #include <string.h>
 
@@ -64,7 +63,7 @@ __device__ __forceinline__ void fm_gateup_load(const FmSlot &s, uint32_t row, ui
 }
 
 template <int BITS, int LPR, int GPL>
-__device__ __forceinline__ void fm_gateup_segment(const FmDecodeArgs &a, const FmSlot &s, int slot,
+__device__ __forceinline__ void fm_gateup_segment(const FmDecodeArgs &a, uint32_t ep, const FmSlot &s, int slot,
                                                   const float *xs, uint32_t ubeg, uint32_t uend) {
     constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -92,7 +91,7 @@ __device__ __forceinline__ void fm_gateup_segment(const FmDecodeArgs &a, const F
         }
         pg = fm_lane_sum<LPR>(pg);
         pu = fm_lane_sum<LPR>(pu);
-        if (gl == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)slot * a.inter + row], fm_silu_mul(pg, pu), a.epoch);
+        if (gl == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)slot * a.inter + row], fm_silu_mul(pg, pu), ep);
         cur = nxt;
     }
 }
@@ -129,7 +128,7 @@ __device__ __forceinline__ void fm_down_load(const FmSlot &s, uint32_t row, uint
 // y[row] for rows of passes [pbeg, pend) of one slot; writes `dst` (fp32,
 // indexed by row) from the first lane of each row segment.
 template <int BITS, int LPR, int GPL>
-__device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmSlot &s, int slot,
+__device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, uint32_t ep, const FmSlot &s, int slot,
                                                 uint32_t pbeg, uint32_t pend, float *dst, float *wbuf) {
     constexpr int RPP = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -143,11 +142,11 @@ __device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmS
     const uint64_t *act = a.act2 + (size_t)slot * a.inter;
     for (uint32_t i0 = 0; i0 < a.inter; i0 += 64) {
         const uint32_t i = i0 + lane;
-        uint64_t v = i < a.inter ? fm_get_tagged(act + i) : ((uint64_t)a.epoch << 32);
+        uint64_t v = i < a.inter ? fm_get_tagged(act + i) : ((uint64_t)ep << 32);
         uint32_t it = 0;
-        while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+        while (!__all((uint32_t)(v >> 32) == ep) && ++it < FM_SPIN_MAX) {
             __builtin_amdgcn_s_sleep(1);
-            if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(act + i);
+            if ((uint32_t)(v >> 32) != ep) v = fm_get_tagged(act + i);
         }
         if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
         if (i < a.inter) wbuf[i] = __uint_as_float((uint32_t)v);
@@ -175,7 +174,7 @@ __device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmS
             if (a.mode == 1)
                 dst[row] = part;
             else
-                fm_put_tagged(&a.y2[(size_t)slot * a.hidden + row], part, a.epoch);
+                fm_put_tagged(&a.y2[(size_t)slot * a.hidden + row], part, ep);
         }
         cur = nxt;
     }
@@ -194,7 +193,7 @@ __device__ __forceinline__ void fm_down_segment(const FmDecodeArgs &a, const FmS
 // in the slot order of cpu_vec_madd (layer_forward.h:1257, 1295-1305), polling
 // the other slots' tagged y words for the pass's rows first.
 template <int RPP>
-__device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, const FmSlot *sd, uint32_t row0, float sw,
+__device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, uint32_t ep, const FmSlot *sd, uint32_t row0, float sw,
                                                 float *stage) {
     const int lane = threadIdx.x & 63;
     const int n = (a.S - 1) * RPP;  // values to collect from other slots
@@ -202,11 +201,11 @@ __device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, const FmS
         const int q = base + lane;
         const int k = q / RPP, r = q % RPP;
         const bool need = q < n && sd[k].valid && row0 + r < a.hidden;
-        uint64_t v = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]) : ((uint64_t)a.epoch << 32);
+        uint64_t v = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]) : ((uint64_t)ep << 32);
         uint32_t it = 0;
-        while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+        while (!__all((uint32_t)(v >> 32) == ep) && ++it < FM_SPIN_MAX) {
             __builtin_amdgcn_s_sleep(1);
-            if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]);
+            if ((uint32_t)(v >> 32) != ep) v = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row0 + r]);
         }
         if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
         if (q < n) stage[q] = need ? __uint_as_float((uint32_t)v) : 0.f;
@@ -235,9 +234,12 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
     // LDS: x (hidden floats), then one inter-float buffer per wave
     extern __shared__ float xs[];
     __shared__ FmSlot sd[FM_MAX_SLOTS];
+    __shared__ uint32_t ep_s;
+    if (threadIdx.x == 0) ep_s = fm_epoch_read(a);
     if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
     for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
     __syncthreads();
+    const uint32_t ep = ep_s;
     const int lane = threadIdx.x & 63;
     const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
     float *wbuf = xs + a.hidden + (threadIdx.x >> 6) * a.inter;
@@ -254,9 +256,9 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
         if (s.valid) {
             const uint32_t b = u - k * upsA, e = seg_end - k * upsA;
             if (s.bits == 4)
-                fm_gateup_segment<4, LH, GH>(a, s, k, xs, b, e);
+                fm_gateup_segment<4, LH, GH>(a, ep, s, k, xs, b, e);
             else
-                fm_gateup_segment<2, LH, GH>(a, s, k, xs, b, e);
+                fm_gateup_segment<2, LH, GH>(a, ep, s, k, xs, b, e);
         }
         u = seg_end;
     }
@@ -275,9 +277,9 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
         if (s.valid) {
             float *dst = a.mode == 1 ? a.expert_out + (size_t)k * a.hidden : nullptr;
             if (s.bits == 4)
-                fm_down_segment<4, LI, GI>(a, s, k, pb, pe, dst, wbuf);
+                fm_down_segment<4, LI, GI>(a, ep, s, k, pb, pe, dst, wbuf);
             else
-                fm_down_segment<2, LI, GI>(a, s, k, pb, pe, dst, wbuf);
+                fm_down_segment<2, LI, GI>(a, ep, s, k, pb, pe, dst, wbuf);
         }
         if (a.mode == 0 && k == a.S - 1) {
             for (uint32_t p = pb; p < pe; p++) {
@@ -285,21 +287,23 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
                 if (s.valid) {
                     const uint32_t row = p * RPPB + (lane < RPPB ? lane : 0);
                     uint64_t t = lane < RPPB && row < a.hidden ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row])
-                                                               : ((uint64_t)a.epoch << 32);
+                                                               : ((uint64_t)ep << 32);
                     uint32_t it = 0;
-                    while (!__all((uint32_t)(t >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
+                    while (!__all((uint32_t)(t >> 32) == ep) && ++it < FM_SPIN_MAX) {
                         __builtin_amdgcn_s_sleep(1);
-                        if ((uint32_t)(t >> 32) != a.epoch) t = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]);
+                        if ((uint32_t)(t >> 32) != ep) t = fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]);
                     }
                     if (lane < RPPB) wbuf[(a.S - 1) * RPPB + lane] = __uint_as_float((uint32_t)t);
                 } else if (lane < RPPB) {
                     wbuf[(a.S - 1) * RPPB + lane] = 0.f;
                 }
-                fm_combine_pass<RPPB>(a, sd, p * RPPB, sw, wbuf);
+                fm_combine_pass<RPPB>(a, ep, sd, p * RPPB, sw, wbuf);
             }
         }
         v = seg_end;
     }
+    __syncthreads();
+    if (threadIdx.x == 0) fm_epoch_finish(a, ep, gridDim.x);
 }
 
 // ------------------------------------------------- fused kernel, eager loads --
@@ -408,11 +412,14 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
     constexpr int RPPA = 64 / LH, RPPB = 64 / LI;
     extern __shared__ float xs[];  // x [hidden] | act [2][inter] | combine stage [4][S*RPPB]
     __shared__ FmSlot sd[FM_MAX_SLOTS];
+    __shared__ uint32_t ep_s;
     float *acts = xs + a.hidden;
     float *stage_all = acts + 2 * a.inter;
+    if (threadIdx.x == 0) ep_s = fm_epoch_read(a);
     if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
     for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
     __syncthreads();
+    const uint32_t ep = ep_s;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t w = blockIdx.x * 4 + wv;
     const int subA = lane / LH, glA = lane % LH;
@@ -468,7 +475,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                 }
                 pg = fm_lane_sum<LH>(pg);
                 pu = fm_lane_sum<LH>(pu);
-                if (glA == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)k * a.inter + row], fm_silu_mul(pg, pu), a.epoch);
+                if (glA == 0 && row < a.inter) fm_put_tagged(&a.act2[(size_t)k * a.inter + row], fm_silu_mul(pg, pu), ep);
             }
         }
         // issue down-projection unit i's loads (independent of act) between
@@ -502,20 +509,20 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
             const uint32_t i = q * 256 + threadIdx.x;
             const int kk = kb0 + (int)(i / a.inter);
             const bool need = i < total && sd[kk].valid;
-            t[q] = need ? fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i) : ((uint64_t)a.epoch << 32);
+            t[q] = need ? fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i) : ((uint64_t)ep << 32);
         }
         uint32_t it = 0;
         bool ready;
         do {
             ready = true;
 #pragma unroll
-            for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == a.epoch;
+            for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == ep;
             if (__all(ready)) break;
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int q = 0; q < MAXQ; q++) {
                 const uint32_t i = q * 256 + threadIdx.x;
-                if ((uint32_t)(t[q] >> 32) != a.epoch) t[q] = fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i);
+                if ((uint32_t)(t[q] >> 32) != ep) t[q] = fm_get_tagged(a.act2 + (size_t)kb0 * a.inter + i);
             }
         } while (++it < FM_SPIN_MAX);
         if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
@@ -554,7 +561,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                     if (a.mode == 1)
                         a.expert_out[(size_t)k * a.hidden + row] = y;
                     else if (k != a.S - 1)
-                        fm_put_tagged(&a.y2[(size_t)k * a.hidden + row], y, a.epoch);
+                        fm_put_tagged(&a.y2[(size_t)k * a.hidden + row], y, ep);
                 }
             }
             if (a.mode == 0 && k == a.S - 1 && glB == 0) stage[i * a.S * RPPB + (a.S - 1) * RPPB + subB] = y;
@@ -581,18 +588,18 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                 const int k = rem / RPPB, r = rem % RPPB;
                 const uint32_t row = (lb + ui - kl * upsB) * RPPB + r;
                 const bool need = e < n && sd[k].valid && row < a.hidden;
-                t[q] = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]) : ((uint64_t)a.epoch << 32);
+                t[q] = need ? fm_get_tagged(&a.y2[(size_t)k * a.hidden + row]) : ((uint64_t)ep << 32);
             }
             uint32_t it = 0;
             do {
                 bool ready = true;
 #pragma unroll
-                for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == a.epoch;
+                for (int q = 0; q < MAXQ; q++) ready &= (uint32_t)(t[q] >> 32) == ep;
                 if (__all(ready)) break;
                 __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (int q = 0; q < MAXQ; q++) {
-                    if ((uint32_t)(t[q] >> 32) != a.epoch) {
+                    if ((uint32_t)(t[q] >> 32) != ep) {
                         const int e = q * 64 + lane;
                         const int ui = e / per, rem = e % per;
                         const int k = rem / RPPB, r = rem % RPPB;
@@ -633,6 +640,8 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
         }
     }
     FM_DX_MARK(6);
+    __syncthreads();
+    if (threadIdx.x == 0) fm_epoch_finish(a, ep, gridDim.x);
 }
 
 // ---------------------------------------------------------------- combine --
@@ -650,6 +659,25 @@ __global__ __launch_bounds__(256) void fm_combine_kernel(const float *h_mid, con
     if (so) v = __fadd_rn(v, __fmul_rn(score ? fm_sigmoid(*score) : 1.0f, so[i]));
     out[i] = v;
     if (out_bf16) out_bf16[i] = fm_f32_to_bf16(v);
+}
+
+// Zero fill of a workspace (a kernel, not hipMemsetAsync, so a caller may
+// record it into a graph).
+__global__ __launch_bounds__(256) void fm_ws_zero_kernel(fm_u4 *p, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+        p[i] = (fm_u4){0u, 0u, 0u, 0u};
+}
+
+extern "C" int fm_workspace_init(void *ws, size_t ws_bytes, void *stream) {
+    fm_clear_error();
+    FM_REQUIRE(ws, "fm_workspace_init: NULL workspace");
+    if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "fm_workspace_init: workspace not 256-byte aligned");
+    const size_t n16 = ws_bytes / 16;
+    if (n16 == 0) return FM_OK;
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fm_ws_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, fm_stream(stream), (fm_u4 *)ws, n16);
+    return fm_check_launch("fm_ws_zero_kernel");
 }
 
 // ---------------------------------------------------------------- host -----
@@ -679,20 +707,14 @@ static int fm_check_expert(const char *who, int k, const fm_expert_weights &e, i
     return FM_OK;
 }
 
-// Workspace: [err word, 256 B] [act2: S x inter x 8 B] [y2: S x hidden x 8 B]
+// Workspace: [header, 256 B: status word, epoch, finished-unit count]
+// [act2: S x inter x 8 B] [y2: S x hidden x 8 B]
 // [ss2: hidden/64 x 8 B tagged partial sums of squares for the fused RMS norm]
-// Tags make stale contents harmless, so the workspace needs no initialisation.
+// It starts zeroed (fm_workspace_init); tags make stale contents harmless after that.
 extern "C" size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter) {
     if (n_slots < 1) n_slots = 1;
     return 256 + fm_align_up((size_t)n_slots * inter * 8, 256) + fm_align_up((size_t)n_slots * hidden * 8, 256) +
            fm_align_up((size_t)(hidden + 63) / 64 * 8, 256);
-}
-
-static uint32_t fm_next_epoch() {
-    static std::atomic<uint32_t> ctr{0};
-    uint32_t e = ctr.fetch_add(1) + 1;
-    if (e == 0) e = ctr.fetch_add(1) + 1;  // 0 never tags anything
-    return e;
 }
 
 template <int LH, int GH, int LI, int GI>
@@ -770,7 +792,8 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     a.y2 = (uint64_t *)p;
     p += fm_align_up((size_t)a.S * a.hidden * 8, 256);
     a.ss2 = (uint64_t *)p;
-    a.epoch = fm_next_epoch();
+    a.ws_epoch = (uint32_t *)((char *)ws + FM_WS_EPOCH_OFF);
+    a.ws_done = (uint32_t *)((char *)ws + FM_WS_DONE_OFF);
     if (a.ntok > 1)  // several tokens in one launch: only the mfma kernel implements it
         return fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st)
                                          : fm_fail(FM_ERR_UNSUPPORTED, "%s: several tokens need the mfma kernel", who);

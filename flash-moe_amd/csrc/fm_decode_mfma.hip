@@ -68,6 +68,7 @@ struct __attribute__((aligned(16))) FmmLds {
     uint8_t tbits[FMM_TAB];             // prologue: pool bit widths
     float part[4][16][2];     // per-wave partial gate/up sums of the A rows
     float ylast[64];          // this block's rows of the last slot's y
+    uint32_t ep;              // this call's tag
     uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
     FmSlot sd[NSLOT];
 };
@@ -338,6 +339,9 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     };
 
     FM_DX_MARK(0);
+    // this call's tag: read first, written to LDS only at the prologue's last barrier
+    uint32_t ep_rd = 0;
+    if (tid == 0) ep_rd = fm_epoch_read(a);
     // x first: thread t holds elements 16*(t%4) .. +15 of group t/4.  Loaded
     // before the slot lookup and the weights, so its latency overlaps theirs.
     fm_f4 xr[4];
@@ -384,7 +388,9 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
         L.sd[tid] = fm_get_slot(a, sK, sT);
     }
     if (tid < 32) L.zero[tid] = fm_as_h2(0u);
+    if (tid == 0) L.ep = ep_rd;
     __syncthreads();
+    const uint32_t ep = L.ep;
 
     for (uint32_t b = b0; b < nitems; b += gridDim.x) {
     // The arguments are re-read from the kernarg segment per item (scalar
@@ -395,7 +401,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     int tid = threadIdx.x;
     if constexpr (MP) asm volatile("" : "+v"(tid));
     const int lane = tid & 63, wv = tid >> 6, n = lane & 15, q = lane >> 4;
-    const int spt = a.spt, ph = a.phases ? a.phases : 3;
+    const int spt = a.spt;
     const uint32_t H = a.hidden, I = a.inter, GI = I / 64, tilesA = I / 16, tilesB = H / 64;
     if (b != b0) load_x(b);
     const bool hasA = b < (uint32_t)a.S * tilesA;
@@ -406,7 +412,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     const FmSlot sA = MP ? fmm_uniform(L.sd[kA]) : L.sd[kA];
     FmSlot sB;
     if constexpr (!MP) sB = L.sd[kB];
-    const bool doA = (ph & 1) && hasA && sA.valid;
+    const bool doA = hasA && sA.valid;
     // ---- issue every weight load of this wave ----
     const uint32_t rowA0 = (b % tilesA) * 16;
     FmmCodes cg, cu, cdn;
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     if (doA && tid < 16) {
         const float g = (L.part[0][tid][0] + L.part[1][tid][0]) + (L.part[2][tid][0] + L.part[3][tid][0]);
         const float u = (L.part[0][tid][1] + L.part[1][tid][1]) + (L.part[2][tid][1] + L.part[3][tid][1]);
-        fm_put_tagged(&a.act2[(size_t)kA * I + rowA0 + tid], fm_silu_mul(g, u), a.epoch);
+        fm_put_tagged(&a.act2[(size_t)kA * I + rowA0 + tid], fm_silu_mul(g, u), ep);
     }
 
     FM_DX_MARK(4);
@@ -494,7 +500,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     // the slot's activations exist, and issuing them early would only delay
     // other waves' gate/up data.
     if constexpr (MP) sB = fmm_uniform(L.sd[kB]);  // read only now: fewer registers live during A
-    const bool doB = (ph & 2) && hasB && sB.valid;
+    const bool doB = hasB && sB.valid;
     fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn, lane);
     // ---- B: stage the slot's activations, then 16 down rows per wave ----
     if (doB) {
@@ -504,18 +510,18 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
 #pragma unroll
         for (int j = 0; j < MAXQ; j++) {
             const uint32_t i = j * 256 + tid;
-            t[j] = i < I ? fm_get_tagged(src + i) : ((uint64_t)a.epoch << 32);
+            t[j] = i < I ? fm_get_tagged(src + i) : ((uint64_t)ep << 32);
         }
         uint32_t it = 0;
         do {
             bool ready = true;
 #pragma unroll
-            for (int j = 0; j < MAXQ; j++) ready &= (uint32_t)(t[j] >> 32) == a.epoch;
+            for (int j = 0; j < MAXQ; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
             if (__all(ready)) break;
 #pragma unroll
             for (int j = 0; j < MAXQ; j++) {
                 const uint32_t i = j * 256 + tid;
-                if ((uint32_t)(t[j] >> 32) != a.epoch) t[j] = fm_get_tagged(src + i);
+                if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(src + i);
             }
         } while (++it < FM_SPIN_MAX);
         if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
@@ -548,7 +554,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     }
     __syncthreads();
     FM_DX_MARK(5);
-    const bool last = (ph & 2) && hasB && a.mode == 0 && kB % spt == spt - 1;
+    const bool last = hasB && a.mode == 0 && kB % spt == spt - 1;
     if (doB) {
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &L.aq[sB.bits == 4 ? 0 : 1][0][0];
@@ -563,7 +569,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             if (a.mode == 1)
                 a.expert_out[(size_t)kB * H + row] = y;
             else if (!last)
-                fm_put_tagged(&a.y2[(size_t)kB * H + row], y, a.epoch);
+                fm_put_tagged(&a.y2[(size_t)kB * H + row], y, ep);
             else
                 L.ylast[16 * wv + n] = y;
         }
@@ -584,16 +590,16 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
 #pragma unroll
             for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
                 t[k] = (k < spt - 1 && L.sd[k0 + k].valid) ? fm_get_tagged(&a.y2[(size_t)(k0 + k) * H + row])
-                                                         : ((uint64_t)a.epoch << 32);
+                                                         : ((uint64_t)ep << 32);
             uint32_t it = 0;
             do {
                 bool ready = true;
 #pragma unroll
-                for (int k = 0; k < FM_MAX_SLOTS - 1; k++) ready &= (uint32_t)(t[k] >> 32) == a.epoch;
+                for (int k = 0; k < FM_MAX_SLOTS - 1; k++) ready &= (uint32_t)(t[k] >> 32) == ep;
                 if (__all(ready)) break;
 #pragma unroll
                 for (int k = 0; k < FM_MAX_SLOTS - 1; k++)
-                    if ((uint32_t)(t[k] >> 32) != a.epoch) t[k] = fm_get_tagged(&a.y2[(size_t)(k0 + k) * H + row]);
+                    if ((uint32_t)(t[k] >> 32) != ep) t[k] = fm_get_tagged(&a.y2[(size_t)(k0 + k) * H + row]);
             } while (++it < FM_SPIN_MAX);
             if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
             const float sw =
@@ -618,11 +624,11 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
                 // then reduces all of them in the same fixed order
                 const uint32_t j = b % tilesB;
                 const float sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(o * o))));
-                if (lane == 0) fm_put_tagged(&a.ss2[j], sq, a.epoch);
-                uint64_t v = lane < (int)tilesB ? fm_get_tagged(&a.ss2[lane]) : ((uint64_t)a.epoch << 32);
+                if (lane == 0) fm_put_tagged(&a.ss2[j], sq, ep);
+                uint64_t v = lane < (int)tilesB ? fm_get_tagged(&a.ss2[lane]) : ((uint64_t)ep << 32);
                 uint32_t it = 0;
-                while (!__all((uint32_t)(v >> 32) == a.epoch) && ++it < FM_SPIN_MAX) {
-                    if ((uint32_t)(v >> 32) != a.epoch) v = fm_get_tagged(&a.ss2[lane]);
+                while (!__all((uint32_t)(v >> 32) == ep) && ++it < FM_SPIN_MAX) {
+                    if ((uint32_t)(v >> 32) != ep) v = fm_get_tagged(&a.ss2[lane]);
                 }
                 if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
                 const float part = lane < (int)tilesB ? __uint_as_float((uint32_t)v) : 0.f;
@@ -633,6 +639,10 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
         }
     }
     FM_DX_MARK(7);
+    // the ends of the hand-off chains: combining items (mode 0) or every down
+    // item (mode 1, per-slot outputs) count towards publishing the next epoch
+    if (tid == 0 && (a.mode == 0 ? last : hasB))
+        fm_epoch_finish(a, ep, (uint32_t)(a.mode == 0 ? a.ntok : a.S) * tilesB);
     __syncthreads();  // LDS of this item is reused by the next
     if constexpr (!MP) break;
     }

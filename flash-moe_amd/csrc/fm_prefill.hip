@@ -805,8 +805,10 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     const size_t nent = (size_t)T * K + (has_shared ? T : 0);
     const uint32_t mc = pf_max_chunks(T, K, E, has_shared);
     size_t o = 0;
-    L.err = o;  // status word first (fm_workspace_status)
-    o += 256;
+    L.err = o;  // header first: status word (fm_workspace_status), decode epoch
+    // the decode kernels' tagged region for the few-token paths (T <= 8): kept
+    // apart from the GEMM arrays below, so it only ever holds tagged words
+    o = fm_moe_decode_workspace_size(FM_PREFILL_DECODE_MAX_T * (FM_MAX_K + 1), hidden, inter);
     L.entries = o;
     o += fm_align_up(nent * 4, 256);
     L.chunks = o;
@@ -829,12 +831,7 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
 
 extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool) {
     if (!pool || T <= 0 || K <= 0) return 0;
-    size_t n = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
-    if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K) {  // room for the one-launch decode of a few tokens
-        const size_t d = fm_moe_decode_tokens_workspace_size(T, K, 1, pool->hidden, pool->inter);
-        if (d > n) n = d;
-    }
-    return n;
+    return pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
 }
 
 static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,

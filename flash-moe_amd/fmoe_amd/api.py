@@ -16,10 +16,11 @@ __all__ = [
     "prefill_workspace_bytes", "prefill_moe", "pfb_gemm", "DevicePool", "moe_forward",
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
     "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
-    "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS",
+    "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS", "STATUS_EPOCH_WRAP", "workspace_init",
+    "workspace",
 ]
 
-STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS = 1, 2, 4
+STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP = 1, 2, 4, 8
 
 
 def _i32_array(vals):
@@ -105,6 +106,19 @@ def workspace_status(ws, stream=None):
     v = ctypes.c_uint32()
     check(lib().fm_workspace_status(ptr(ws), ctypes.byref(v), stream_ptr(stream)))
     return v.value
+
+
+def workspace_init(ws, stream=None):
+    """Zero a workspace with the library's fill kernel (fm_workspace_init)."""
+    check(lib().fm_workspace_init(ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def workspace(nbytes, device, stream=None):
+    """A freshly allocated, initialised (zeroed) device workspace of nbytes."""
+    import torch
+    ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+    workspace_init(ws, stream)
+    return ws
 
 
 def rms_norm(x, w_bf16, eps, out, out_bf16=None, stream=None):

@@ -94,9 +94,10 @@ size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
     n += align256((size_t)T * sizeof(float));                             /* seg scores */
     n += align256((size_t)T * K * sizeof(int));
     n += align256((size_t)T * K * sizeof(float));
-    size_t g1 = fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden);
-    size_t g2 = fm_prefill_moe_workspace_size(T, K, &L->pool);
-    return n + align256(g1 > g2 ? g1 : g2);
+    /* the expert step's region (its header and decode-tagged words first) and
+     * the router GEMM's region are disjoint: the GEMM never overwrites tags */
+    n += align256(fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden));
+    return n + align256(fm_prefill_moe_workspace_size(T, K, &L->pool));
 }
 
 int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
@@ -106,11 +107,11 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     if (T <= 0 || !h_post || !out) return fm_host_fail(FM_ERR_INVALID, "fm_moe_prefill_forward: T <= 0 or NULL buffer");
     size_t need = fm_moe_prefill_workspace_size(L, K, T);
     if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_prefill_forward: workspace too small");
-    /* [router GEMM / expert step region: status word first][logits][seg][idx][w] */
-    size_t g1 = fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden);
-    size_t g2 = fm_prefill_moe_workspace_size(T, K, &L->pool);
-    const size_t step = align256(g1 > g2 ? g1 : g2);
-    char *p = (char *)ws + step;
+    /* [expert step region: header first][router GEMM region][logits][seg][idx][w] */
+    const size_t step = align256(fm_prefill_moe_workspace_size(T, K, &L->pool));
+    const size_t gemm = align256(fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden));
+    char *g = (char *)ws + step;
+    char *p = g + gemm;
     float *logits = (float *)p;
     p += align256((size_t)T * L->pool.num_experts * sizeof(float));
     float *seg = (float *)p;
@@ -124,11 +125,11 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     /* routing gate and shared_expert_gate over all tokens (batched_prefill.h:164-182) */
     int rc = fm_pfb_gemm(L->router_w, L->router_s, L->router_b, h_post, logits, (uint32_t)T,
                          L->pool.num_experts, L->pool.hidden, L->pool.group_size, L->router_bits,
-                         p, rest, stream);
+                         g, gemm, stream);
     if (rc) return rc;
     if (L->has_shared) {
         rc = fm_pfb_gemm(L->seg_w, L->seg_s, L->seg_b, h_post, seg, (uint32_t)T, 1, L->pool.hidden,
-                         L->pool.group_size, L->seg_bits, p, rest, stream);
+                         L->pool.group_size, L->seg_bits, g, gemm, stream);
         if (rc) return rc;
     }
     /* per-token softmax / top-K / renormalise (batched_prefill.h:256-261) */

@@ -121,22 +121,30 @@ int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *
 
 /* Workspace bytes for fm_moe_decode / fm_moe_decode_pool(_norm) /
  * fm_encode_experts_batched with n_slots = K (+1 if a shared expert).
- * The workspace must be 256-byte aligned and needs no initialisation: values
- * handed between waves carry a per-call tag, so stale contents are ignored.
+ * The workspace must be 256-byte aligned and start zeroed (fm_workspace_init
+ * once after allocation).  Values handed between workgroups carry a per-call
+ * tag that the kernels keep in the workspace header, on the device, so stale
+ * contents are ignored and a call recorded into a HIP graph may be replayed.
+ * Between calls nothing else may write the workspace (or re-initialise it).
  * Calls that share one workspace must be ordered (same stream); concurrent
  * calls need their own. */
 size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
+
+/* Zero a decode / prefill / layer workspace (ws_bytes rounded down to 16 B)
+ * with a kernel on `stream` (no hipMemsetAsync: recordable into a graph). */
+int fm_workspace_init(void *ws, size_t ws_bytes, void *stream);
 
 /* Status word kept in the first 4 bytes of a decode or prefill workspace
  * (fm_moe_decode*, fm_prefill_moe, fm_moe_forward*, fm_moe_prefill_forward):
  * the kernels OR in FM_STATUS_* bits and never clear them.  This call waits for
  * the work queued on `stream`, returns the accumulated bits in *status and
  * clears them.  A freshly allocated workspace holds arbitrary bits: clear it
- * once with this call before relying on it.  The reference only printed
+ * once with this call (or fm_workspace_init) before relying on it.  The reference only printed
  * (e.g. "WARNING: expert %d pread" in expert_io.h:314); here the caller can ask. */
 #define FM_STATUS_WAIT_TIMEOUT 1u  /* a bounded wait between workgroups gave up: output invalid */
 #define FM_STATUS_BAD_EXPERT 2u    /* a routed expert index outside the pool was skipped */
 #define FM_STATUS_CHUNKS 4u        /* prefill: more expert chunks than the workspace holds */
+#define FM_STATUS_EPOCH_WRAP 8u    /* the per-call tag wrapped after 2^32 - 1 calls: fm_workspace_init needed */
 int fm_workspace_status(void *ws, uint32_t *status, void *stream);
 
 /* K expert FFNs sharing input x, one output per expert:

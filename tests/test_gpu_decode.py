@@ -107,7 +107,7 @@ def test_moe_decode_host_routed(orc, dev, K, bitmode, hidden, inter):
     blobs, x, hm, w, score = _decode_inputs(K + hidden // 512, K, bl, hidden, inter)
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, bl[i], hidden, inter) for i, db in enumerate(dblobs)]
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, hidden, inter), dev)
     out = torch.empty(hidden, dtype=torch.float32, device=dev)
     ob = torch.empty(hidden, dtype=torch.int16, device=dev)
     fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, hidden, inter, shared=ex[K], shared_bits=bl[K],
@@ -130,7 +130,7 @@ def test_moe_decode_valid_mask_and_no_shared(orc, dev):
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, 4, HIDDEN, INTER) for db in dblobs]
     valid = [1, 0, 1, 1, 0, 1]
-    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, valid=valid)
     torch.cuda.synchronize()
@@ -146,7 +146,7 @@ def test_encode_experts_batched_and_combine(orc, dev):
     blobs, x, hm, w, score = _decode_inputs(12, K, bl)
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     eo = torch.zeros((K + 1, HIDDEN), dtype=torch.float32, device=dev)
     fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
     torch.cuda.synchronize()
@@ -188,7 +188,7 @@ def test_moe_decode_pool_device_routing(orc, dev, pool64):
     idx = torch.empty((1, K), dtype=torch.int32, device=dev)
     w = torch.empty((1, K), dtype=torch.float32, device=dev)
     fm.route_topk(T(lg, dev), K, idx, w)
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode_pool(pool, idx, w, T(x, dev), out, ws, shared=sh, shared_bits=4,
                        shared_score=T(np.array([g]), dev), h_mid=T(hm, dev))
@@ -223,7 +223,7 @@ def test_moe_forward_layer(orc, dev, pool64):
     L.shared_bits = 4
     L.has_shared = 1
     L.pool = pool.c
-    ws = torch.zeros(fm.moe_forward_workspace_bytes(L, K), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.moe_forward_workspace_bytes(L, K), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_forward(L, K, T(hp, dev), T(hm, dev), out, ws)
     torch.cuda.synchronize()
@@ -275,7 +275,7 @@ def test_moe_decode_pool_norm(orc, dev, hidden, inter):
     idx = torch.empty((1, K), dtype=torch.int32, device=dev)
     wt = torch.empty((1, K), dtype=torch.float32, device=dev)
     fm.route_topk(T(lg, dev), K, idx, wt)
-    ws = torch.empty(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, hidden, inter), dev)
     out = torch.empty(hidden, dtype=torch.float32, device=dev)
     normed = torch.empty(hidden, dtype=torch.float32, device=dev)
     for rep in range(2):  # a second call on the same workspace (stale tags must not leak)
@@ -298,7 +298,7 @@ def test_moe_decode_repeated_calls_one_workspace(orc, dev):
     call's, including when the slot count and bit widths change."""
     import torch
     say("moe_decode repeated calls")
-    ws = torch.zeros(fm.decode_workspace_bytes(11, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(11, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     for rep, (K, bl) in enumerate([(10, [4] * 11), (10, [2, 4] * 5 + [4]), (5, [4, 2, 2, 4, 4, 2]), (10, [4] * 11)]):
         blobs, x, hm, w, score = _decode_inputs(500 + rep, K, bl)
@@ -337,7 +337,7 @@ def test_moe_decode_pool_large_expert_count(orc, dev):
     ri, rw = orc.route(lg, K)
     x = synth.hidden_vec(rng, HIDDEN)
     hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
-    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode_pool(pool, T(ri[0].astype(np.int32), dev), T(rw[0], dev), T(x, dev), out, ws, h_mid=T(hm, dev))
     torch.cuda.synchronize()
@@ -355,7 +355,7 @@ def test_workspace_status_bad_expert(orc, dev, pool64):
     K = 4
     rng = synth.rng_for(43)
     x = synth.hidden_vec(rng, HIDDEN)
-    ws = torch.empty(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.workspace_status(ws)  # a fresh workspace holds arbitrary bits
     w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)

@@ -35,7 +35,7 @@ def pool64():
 
 def _per_token(pool, idx, w, X, hm, g, sh, dev, K):
     import torch
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     outs = []
     for t in range(idx.shape[0]):
         o = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
@@ -60,7 +60,7 @@ def test_few_tokens_one_launch(orc, dev, pool64, Tn, K):
     sh_blob = synth.expert_blob((8802, 0), HIDDEN, INTER, 4)
     dsh = T(sh_blob, dev)
     sh = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     fm.workspace_status(ws)  # clears the status word of the fresh workspace
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     ob = torch.empty((Tn, HIDDEN), dtype=torch.int16, device=dev)
@@ -94,7 +94,7 @@ def test_few_tokens_bad_expert_skipped(orc, dev, pool64):
     X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
     bad = idx.copy()
     bad[2, 3] = 64
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     fm.workspace_status(ws)  # clears the status word of the fresh workspace
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     fm.prefill_moe(pool, T(bad, dev), T(w, dev), T(X, dev), out, ws)
@@ -121,7 +121,7 @@ def test_single_token_17_slots(orc, dev, pool64):
     sh_blob = synth.expert_blob((8805, 0), HIDDEN, INTER, 2)
     dsh = T(sh_blob, dev)
     sh = fm.experts_from_blob(dsh, 2, HIDDEN, INTER)
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     fm.moe_decode_pool(pool, T(idx[0], dev), T(w[0], dev), T(x, dev), out, ws, shared=sh, shared_bits=2,
                        shared_score=T(np.array([0.3], np.float32), dev), h_mid=T(hm, dev))
@@ -149,7 +149,7 @@ def test_few_tokens_optional_args(orc, dev, pool64, Tn, K, shared_bits, with_hmi
         sh_blob = synth.expert_blob((8807, shared_bits), HIDDEN, INTER, shared_bits)
         dsh = T(sh_blob, dev)
         sh = fm.experts_from_blob(dsh, shared_bits, HIDDEN, INTER)
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     fm.workspace_status(ws)
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws, shared=sh, shared_bits=shared_bits or 4,
@@ -157,7 +157,7 @@ def test_few_tokens_optional_args(orc, dev, pool64, Tn, K, shared_bits, with_hmi
     torch.cuda.synchronize()
     assert fm.workspace_status(ws) == 0
     got = out.cpu().numpy()
-    dws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    dws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     o = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     for t in range(Tn):
         fm.moe_decode_pool(pool, T(idx[t], dev), T(w[t], dev), T(X[t], dev), o, dws, shared=sh,

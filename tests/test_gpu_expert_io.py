@@ -56,7 +56,7 @@ def test_load_layer_bytes_and_decode(orc, dev, tiered_model):
         x = synth.hidden_vec(rng, HIDDEN)
         hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
         ri, rw = orc.route(lg, K)
-        ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+        ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
         out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
         fm.moe_decode_pool(lp, T(ri.astype(np.int32), dev), T(rw, dev), T(x, dev), out, ws, h_mid=T(hm, dev))
         torch.cuda.synchronize()
@@ -75,7 +75,7 @@ def test_load_layer_prefill(orc, dev, tiered_model):
         rng = synth.rng_for(22)
         idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
         X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
-        ws = torch.empty(fm.lib().fm_prefill_moe_workspace_size(Tn, K, lp.c), dtype=torch.uint8, device=dev)
+        ws = fm.workspace(fm.lib().fm_prefill_moe_workspace_size(Tn, K, lp.c), dev)
         out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
         fm.prefill_moe(lp, T(idx, dev), T(w, dev), T(X, dev), out, ws)
         torch.cuda.synchronize()
@@ -91,7 +91,7 @@ def test_stage_per_token_then_decode(orc, dev, tiered_model):
     K = 10
     slot = fm.layout_of(HIDDEN, INTER, 64, 4).size
     bufs = torch.empty((K, slot), dtype=torch.uint8, device=dev)
-    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     with ExpertStore(d, 2, E, HIDDEN, INTER, io_threads=8) as st:
         for it, layer in enumerate((0, 1, 0)):
@@ -133,7 +133,7 @@ def test_stage_invalid_expert_is_skipped(orc, dev, tmp_path):
     rng = synth.rng_for(24)
     x = synth.hidden_vec(rng, HIDDEN)
     w = np.array([0.5, 0.3, 0.2], np.float32)
-    ws = torch.zeros(fm.decode_workspace_bytes(K, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     ex = [fm.experts_from_blob(bufs[k], 4, HIDDEN, INTER) for k in range(K)]
     fm.moe_decode(ex, [4] * K, w, T(x, dev), out, ws, HIDDEN, INTER, valid=valid)

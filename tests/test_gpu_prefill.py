@@ -55,7 +55,7 @@ def _prefill_case(orc, dev, E, Tn, K, H, I, bits_of, seed, zipf=False, shared_bi
     shared_blob = synth.expert_blob((seed, 99999), H, I, shared_bits)
     dsh = T(shared_blob, dev)
     sh = fm.experts_from_blob(dsh, shared_bits, H, I)
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     out = torch.empty((Tn, H), dtype=torch.float32, device=dev)
     ob = torch.empty((Tn, H), dtype=torch.int16, device=dev)
     fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws, shared=sh, shared_bits=shared_bits,
@@ -91,7 +91,7 @@ def test_prefill_config3_vs_decode(orc, dev):
     r = _prefill_case(orc, dev, E, Tn, K, HIDDEN, INTER, lambda e: 4, seed=3, zipf=True)
     counts = np.bincount(r["idx"].reshape(-1), minlength=E)
     assert counts.max() > 100  # skewed
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     for t in (0, 1, 77, 255, 511):
         ex = [r["pool"].expert(int(e)) for e in r["idx"][t]]
@@ -127,7 +127,7 @@ def test_moe_prefill_forward_layer(orc, dev):
     L.shared_bits = 4
     L.has_shared = 1
     L.pool = pool.c
-    ws = torch.zeros(fm.moe_prefill_workspace_bytes(L, K, Tn), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.moe_prefill_workspace_bytes(L, K, Tn), dev)
     out = torch.empty((Tn, H), dtype=torch.float32, device=dev)
     fm.moe_prefill_forward(L, K, Tn, T(X, dev), T(hm, dev), out, ws)
     torch.cuda.synchronize()
@@ -154,7 +154,7 @@ def test_prefill_large_expert_count(orc, dev):
     rng = synth.rng_for(42)
     idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
     X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, dp), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, dp), dev)
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     fm.prefill_moe(dp, T(idx, dev), T(w, dev), T(X, dev), out, ws)
     torch.cuda.synchronize()
@@ -173,7 +173,7 @@ def test_prefill_status_bad_expert(orc, dev):
     rng = synth.rng_for(44)
     idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
     X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     fm.workspace_status(ws)
     fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws)

@@ -73,7 +73,7 @@ def test_decode_range(orc, dev, regime, hidden, inter):
     w = orc.route(rng.normal(0, 1, 64).astype(np.float32), K)[1][0]
     dblobs = [T(b, dev) for b in blobs]
     ex = [fm.experts_from_blob(db, bl[i], hidden, inter) for i, db in enumerate(dblobs)]
-    ws = torch.zeros(fm.decode_workspace_bytes(K + 1, hidden, inter), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, hidden, inter), dev)
     eo = torch.zeros((K + 1, hidden), dtype=torch.float32, device=dev)
     fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, hidden, inter)
     out = torch.empty(hidden, dtype=torch.float32, device=dev)
@@ -105,7 +105,7 @@ def test_prefill_range(orc, dev, regime, Tn):
     shared_blob = synth.expert_blob((5300, 1), HIDDEN, INTER, 2)
     dsh = T(shared_blob, dev)
     sh = fm.experts_from_blob(dsh, 2, HIDDEN, INTER)
-    ws = torch.empty(fm.prefill_workspace_bytes(Tn, K, pool), dtype=torch.uint8, device=dev)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
     out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
     fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws, shared=sh, shared_bits=2,
                    shared_scores=T(g, dev))
