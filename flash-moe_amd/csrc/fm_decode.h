@@ -93,8 +93,7 @@ __device__ __forceinline__ FmSlot fm_get_slot(const FmDecodeArgs &a, int k, int 
 //   +0   status word (FM_STATUS_* bits, fm_workspace_status)
 //   +64  epoch of the last completed call (0 after fm_workspace_init)
 //   +128 count of the running call's finished units
-// Every workgroup reads the header epoch once before its first barrier and
-// tags with epoch + 1; the workgroups (or work items) that end the hand-off
+// Every wave loads the header epoch at its start and tags with epoch + 1; the workgroups (or work items) that end the hand-off
 // chains -- the combining ones -- bump the count after their last tagged
 // access, and the last one stores the new epoch and clears the count.  Tags
 // only grow, and the tagged region is written only with tags, so after
@@ -111,17 +110,23 @@ __device__ __forceinline__ uint64_t fm_get_tagged(const uint64_t *p) {
 #define FM_WS_EPOCH_OFF 64
 #define FM_WS_DONE_OFF 128
 
-// This call's tag (one thread per workgroup, before the workgroup's first barrier).
-__device__ __forceinline__ uint32_t fm_epoch_read(const FmDecodeArgs &a) {
-    const uint32_t e = __hip_atomic_load(a.ws_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+// The header epoch, loaded by every wave at its start (uniform address: one
+// request per wave) and turned into the call's tag by fm_epoch_tag only where
+// first needed, so no wave stalls on this load before issuing its other loads.
+__device__ __forceinline__ uint32_t fm_epoch_load(const FmDecodeArgs &a) {
+    return __hip_atomic_load(a.ws_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t fm_epoch_tag(uint32_t loaded) {
+    const uint32_t e = __builtin_amdgcn_readfirstlane(loaded) + 1u;
     return e ? e : 1u;
 }
 
 // One thread per counted unit of work, after its last tagged access: the last
 // of `total` units publishes the epoch for the next call.  Counted units must
-// be the ends of every hand-off chain (every workgroup that reads the epoch and
-// tags a word feeds, directly or not, one of them), so when the last one
-// arrives every tag user of this call has read the epoch.
+// be the ends of every hand-off chain (every wave that tags or polls a word
+// feeds, directly or not, one of them), so when the last one arrives every tag
+// user of this call has read the epoch (a wave's load completes before its
+// first tagged access).
 __device__ __forceinline__ void fm_epoch_finish(const FmDecodeArgs &a, uint32_t ep, uint32_t total) {
     if (atomicAdd(a.ws_done, 1u) == total - 1) {
         __hip_atomic_store(a.ws_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -234,12 +234,11 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
     // LDS: x (hidden floats), then one inter-float buffer per wave
     extern __shared__ float xs[];
     __shared__ FmSlot sd[FM_MAX_SLOTS];
-    __shared__ uint32_t ep_s;
-    if (threadIdx.x == 0) ep_s = fm_epoch_read(a);
+    const uint32_t ep_ld = fm_epoch_load(a);
     if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
     for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
     __syncthreads();
-    const uint32_t ep = ep_s;
+    const uint32_t ep = fm_epoch_tag(ep_ld);
     const int lane = threadIdx.x & 63;
     const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
     float *wbuf = xs + a.hidden + (threadIdx.x >> 6) * a.inter;
@@ -412,14 +411,13 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
     constexpr int RPPA = 64 / LH, RPPB = 64 / LI;
     extern __shared__ float xs[];  // x [hidden] | act [2][inter] | combine stage [4][S*RPPB]
     __shared__ FmSlot sd[FM_MAX_SLOTS];
-    __shared__ uint32_t ep_s;
     float *acts = xs + a.hidden;
     float *stage_all = acts + 2 * a.inter;
-    if (threadIdx.x == 0) ep_s = fm_epoch_read(a);
+    const uint32_t ep_ld = fm_epoch_load(a);
     if ((int)threadIdx.x < a.S) sd[threadIdx.x] = fm_get_slot(a, threadIdx.x);
     for (uint32_t i = threadIdx.x * 4; i < a.hidden; i += 1024) *(fm_f4 *)(xs + i) = *(const fm_f4 *)(a.x + i);
     __syncthreads();
-    const uint32_t ep = ep_s;
+    const uint32_t ep = fm_epoch_tag(ep_ld);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t w = blockIdx.x * 4 + wv;
     const int subA = lane / LH, glA = lane % LH;

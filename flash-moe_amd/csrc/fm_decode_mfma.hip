@@ -68,7 +68,6 @@ struct __attribute__((aligned(16))) FmmLds {
     uint8_t tbits[FMM_TAB];             // prologue: pool bit widths
     float part[4][16][2];     // per-wave partial gate/up sums of the A rows
     float ylast[64];          // this block's rows of the last slot's y
-    uint32_t ep;              // this call's tag
     uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
     FmSlot sd[NSLOT];
 };
@@ -339,9 +338,8 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     };
 
     FM_DX_MARK(0);
-    // this call's tag: read first, written to LDS only at the prologue's last barrier
-    uint32_t ep_rd = 0;
-    if (tid == 0) ep_rd = fm_epoch_read(a);
+    // this call's tag: loaded first, needed only after the prologue
+    const uint32_t ep_ld = fm_epoch_load(a);
     // x first: thread t holds elements 16*(t%4) .. +15 of group t/4.  Loaded
     // before the slot lookup and the weights, so its latency overlaps theirs.
     fm_f4 xr[4];
@@ -388,9 +386,8 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
         L.sd[tid] = fm_get_slot(a, sK, sT);
     }
     if (tid < 32) L.zero[tid] = fm_as_h2(0u);
-    if (tid == 0) L.ep = ep_rd;
     __syncthreads();
-    const uint32_t ep = L.ep;
+    const uint32_t ep = fm_epoch_tag(ep_ld);
 
     for (uint32_t b = b0; b < nitems; b += gridDim.x) {
     // The arguments are re-read from the kernarg segment per item (scalar
