@@ -22,6 +22,7 @@
 // resolved on the device from routing indices (no host round trip).
 #include "fm_decode.h"
 
+#include <mutex>
 #include <stdlib.h>
 #include <string.h>
 
@@ -947,6 +948,64 @@ extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *
     fm_clear_error();
     return fm_decode_pool_impl("fm_moe_decode_pool", pool, K, idx, weights, shared, shared_bits, shared_gate_score, x,
                                h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream);
+}
+
+// ------------------------------------------------- no-allocation variant --
+// fm_moe_decode_pool_noalloc: the same step with its workspace in a file-scope
+// device array (`scratch`, FM_NOALLOC_WS_BYTES per GPU, held until the process
+// ends) instead of a caller buffer.  The host only ever uses the array's device
+// address from hipGetSymbolAddress, looked up once per device (the array's
+// name in host code is a host-side stand-in, not a device address).  The
+// first call on a device zeroes the array with a kernel; after that the
+// epoch protocol needs no clearing between calls.  Every call on one GPU
+// shares that GPU's array: calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t scratch[FM_NOALLOC_WS_BYTES];
+
+#define FM_NOALLOC_MAX_DEV 64
+static std::mutex fm_noalloc_mu;
+static void *fm_noalloc_ptr[FM_NOALLOC_MAX_DEV];
+
+// Device address of this device's scratch array (set up on first use: symbol
+// lookup, then a zero fill on `st`, ordered before the caller's step).
+static int fm_noalloc_scratch(hipStream_t st, void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= FM_NOALLOC_MAX_DEV)
+        return fm_fail(FM_ERR_HIP, "fm_moe_decode_pool_noalloc: no current device (or device id >= %d)",
+                       FM_NOALLOC_MAX_DEV);
+    std::lock_guard<std::mutex> lock(fm_noalloc_mu);
+    if (!fm_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fm_fail(FM_ERR_HIP, "fm_moe_decode_pool_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        const int rc = fm_workspace_init(p, FM_NOALLOC_WS_BYTES, st);
+        if (rc) return rc;
+        fm_noalloc_ptr[dev] = p;
+    }
+    *out = fm_noalloc_ptr[dev];
+    return FM_OK;
+}
+
+extern "C" size_t fm_noalloc_workspace_bytes(void) { return FM_NOALLOC_WS_BYTES; }
+
+extern "C" int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
+                                          const fm_expert_weights *shared, int shared_bits,
+                                          const float *shared_gate_score, const float *x, const float *h_mid,
+                                          float *out, uint16_t *out_bf16, void *stream) {
+    const char *who = "fm_moe_decode_pool_noalloc";
+    fm_clear_error();
+    FM_REQUIRE(pool, "%s: NULL pool", who);
+    FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
+    const size_t need = fm_moe_decode_workspace_size(K + (shared ? 1 : 0), pool->hidden, pool->inter);
+    if (need > FM_NOALLOC_WS_BYTES)
+        return fm_fail(FM_ERR_UNSUPPORTED, "%s: K=%d, hidden %u, inter %u need a %zu-byte workspace; the static one "
+                       "holds %zu bytes (use fm_moe_decode_pool with a caller workspace)", who, K, pool->hidden,
+                       pool->inter, need, (size_t)FM_NOALLOC_WS_BYTES);
+    void *ws = nullptr;
+    const int rc = fm_noalloc_scratch(fm_stream(stream), &ws);
+    if (rc) return rc;
+    return fm_decode_pool_impl(who, pool, K, idx, weights, shared, shared_bits, shared_gate_score, x, h_mid, out,
+                               out_bf16, nullptr, 0.f, nullptr, ws, FM_NOALLOC_WS_BYTES, stream);
 }
 
 extern "C" int fm_moe_decode_pool_norm(const fm_expert_pool *pool, int K, const int *idx, const float *weights,

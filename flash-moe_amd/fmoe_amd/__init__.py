@@ -94,6 +94,9 @@ SIGNATURES = {
                                       I32, P, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),
     "fm_workspace_status": (I32, [P, ctypes.POINTER(ctypes.c_uint32), P]),
+    "fm_noalloc_workspace_bytes": (ctypes.c_size_t, []),
+    "fm_moe_decode_pool_noalloc": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
+                                         I32, P, P, P, P, P, P]),
     "fm_workspace_init": (I32, [P, ctypes.c_size_t, P]),
     "fm_route_topk": (I32, [P, I32, I32, I32, P, P, P]),
     "fm_prefill_moe_workspace_size": (SZ, [I32, I32, ctypes.POINTER(ExpertPool)]),

@@ -17,7 +17,7 @@ __all__ = [
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
     "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
     "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS", "STATUS_EPOCH_WRAP", "workspace_init",
-    "workspace",
+    "workspace", "moe_decode_pool_noalloc",
 ]
 
 STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP = 1, 2, 4, 8
@@ -90,6 +90,15 @@ def moe_decode_pool(pool, idx, weights, x, out, ws, shared=None, shared_bits=4, 
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
         shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
         ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def moe_decode_pool_noalloc(pool, idx, weights, x, out, shared=None, shared_bits=4, shared_score=None,
+                            h_mid=None, out_bf16=None, stream=None):
+    """fm_moe_decode_pool on the library's static per-GPU workspace (no allocation)."""
+    K = idx.numel()
+    check(lib().fm_moe_decode_pool_noalloc(
+        ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
+        shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), stream_ptr(stream)))
 
 
 def moe_decode_pool_norm(pool, idx, weights, x, out, ws, norm_w, eps, normed, shared=None, shared_bits=4,

@@ -193,6 +193,24 @@ int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
                        const float *x, const float *h_mid, float *out,
                        uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
 
+/* No counterpart in the reference: fm_moe_decode_pool for callers that cannot
+ * allocate device memory (code recorded into a HIP graph, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and result, minus the
+ * workspace: the step uses a file-scope device array of FM_NOALLOC_WS_BYTES per
+ * GPU (held until the process ends; enough for K <= 16 + shared at hidden
+ * 8192 / inter 2048), set up on the first call on each device -- make that
+ * first call outside graph capture.  Calls nothing that allocates.  Shapes
+ * whose workspace exceeds the array return FM_ERR_UNSUPPORTED.  All calls on
+ * one GPU share the array: calls that overlap on one GPU (different streams,
+ * host threads) race and must be serialised by the caller. */
+#define FM_NOALLOC_WS_BYTES (2u << 20)
+size_t fm_noalloc_workspace_bytes(void);
+int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx,
+                               const float *weights, const fm_expert_weights *shared,
+                               int shared_bits, const float *shared_gate_score,
+                               const float *x, const float *h_mid, float *out,
+                               uint16_t *out_bf16, void *stream);
+
 /* fm_moe_decode_pool plus the next layer's input RMS norm of `out` (CMD3 Enc
  * C2/C3, layer_forward.h:3995-4029; rms_norm_sum_sq / rms_norm_apply_bf16,
  * shaders.metal:792-870; CPU semantics cpu_rms_norm, cpu_kernels.h:235-246):
