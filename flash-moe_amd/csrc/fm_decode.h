@@ -34,6 +34,7 @@ struct FmDecodeArgs {
     uint32_t hidden, inter;
     float shared_w_host;       // used when shared_score == NULL and host mode
     const float *shared_score; // device scalar (pre-sigmoid) or NULL
+    const float *shared_y;     // shared expert's output computed by its own launch (own intermediate size), or NULL
     const float *x;
     const float *h_mid;
     float *out;

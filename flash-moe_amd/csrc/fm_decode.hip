@@ -223,6 +223,7 @@ __device__ __forceinline__ void fm_combine_pass(const FmDecodeArgs &a, uint32_t 
         }
         float v = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
         if (a.has_shared) v = __fadd_rn(v, __fmul_rn(sw, ylast));
+        else if (a.shared_y) v = __fadd_rn(v, __fmul_rn(sw, a.shared_y[row]));
         a.out[row] = v;
         if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(v);
     }
@@ -264,7 +265,8 @@ __global__ __launch_bounds__(256) void fm_decode_fused_kernel(FmDecodeArgs a, ui
     }
 
     // ---- B: down projection -> tagged y; the last slot's waves combine ----
-    const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+    const float sw =
+        (a.has_shared || a.shared_y) ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
     const uint32_t upsB = (a.hidden + RPPB - 1) / RPPB;
     const uint64_t NB = (uint64_t)a.S * upsB;
     uint32_t v = (uint32_t)(NB * w / nwaves);
@@ -535,7 +537,8 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
 
     FM_DX_MARK(4);
     // ---- B: down projection -> tagged y (or per-slot outputs) ----
-    const float sw = a.has_shared ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
+    const float sw =
+        (a.has_shared || a.shared_y) ? (a.shared_score ? fm_sigmoid(*a.shared_score) : a.shared_w_host) : 0.f;
     float *stage = stage_all + wv * (FM_UMAX * a.S * RPPB);
     xbits = 0;
     int xslot = -1;
@@ -632,6 +635,7 @@ __global__ __launch_bounds__(256, 2) void fm_decode_eager_kernel(FmDecodeArgs a,
                         if (sd[k].valid) moe = __fadd_rn(moe, __fmul_rn(sd[k].weight, st[k * RPPB + r]));
                     float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
                     if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, st[kl * RPPB + r]));
+                    else if (a.shared_y) o = __fadd_rn(o, __fmul_rn(sw, a.shared_y[row]));
                     a.out[row] = o;
                     if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
                 }
@@ -833,9 +837,57 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     return fm_fail(FM_ERR_UNSUPPORTED, "%s: no kernel instance for hidden %u / inter %u", who, a.hidden, a.inter);
 }
 
+// A shared expert whose intermediate size differs from the routed experts'
+// (config.h:23 shared_intermediate) runs as its own one-slot launch (per-slot
+// output mode) into the workspace tail; the routed step then adds
+// sigmoid(g) * that output in its combine, in the same place of the sum.
+// Workspace: [routed step: K slots][shared launch: 1 slot of shared_inter][shared y]
+static bool fm_shared_apart(int K, int has_shared, uint32_t inter, uint32_t shared_inter) {
+    return has_shared && K > 0 && shared_inter != 0 && shared_inter != inter;
+}
+
+extern "C" size_t fm_moe_decode_workspace_size_ex(int K, int has_shared, uint32_t hidden, uint32_t inter,
+                                                  uint32_t shared_inter) {
+    has_shared = has_shared ? 1 : 0;
+    if (has_shared && K == 0 && shared_inter) return fm_moe_decode_workspace_size(1, hidden, shared_inter);
+    if (!fm_shared_apart(K, has_shared, inter, shared_inter))
+        return fm_moe_decode_workspace_size(K + has_shared, hidden, inter);
+    return fm_moe_decode_workspace_size(K, hidden, inter) + fm_moe_decode_workspace_size(1, hidden, shared_inter) +
+           fm_align_up((size_t)hidden * 4, 256);
+}
+
+// Launches a built step (slot K = the shared expert when has_shared), the
+// shared expert apart when its intermediate size differs (one token only).
+static int fm_decode_launch_shared(FmDecodeArgs &a, uint32_t shared_inter, void *ws, size_t ws_bytes,
+                                   hipStream_t st) {
+    if (a.has_shared && a.K == 0 && shared_inter) a.inter = shared_inter;
+    if (!fm_shared_apart(a.K, a.has_shared, a.inter, shared_inter)) return fm_decode_launch(a, ws, ws_bytes, st);
+    const size_t need = fm_moe_decode_workspace_size_ex(a.K, 1, a.hidden, a.inter, shared_inter);
+    if (!ws || ws_bytes < need)
+        return fm_fail(FM_ERR_WORKSPACE, "fm_moe_decode: workspace %zu bytes < %zu required (shared_inter %u)",
+                       ws_bytes, need, shared_inter);
+    const size_t main = fm_moe_decode_workspace_size(a.K, a.hidden, a.inter);
+    const size_t sub = fm_moe_decode_workspace_size(1, a.hidden, shared_inter);
+    float *shared_y = (float *)((char *)ws + main + sub);
+    FmDecodeArgs b = {};
+    b.slot[0] = a.slot[a.K];
+    b.K = b.S = 1;
+    b.mode = 1;
+    b.hidden = a.hidden;
+    b.inter = shared_inter;
+    b.x = a.x;
+    b.expert_out = shared_y;
+    int rc = fm_decode_launch(b, (char *)ws + main, sub, st);
+    if (rc) return rc;
+    a.has_shared = 0;
+    a.S = a.K;
+    a.shared_y = shared_y;
+    return fm_decode_launch(a, ws, main, st);
+}
+
 extern "C" int fm_moe_decode(int K, const fm_expert_weights *experts, const int *bits,
                              const float *weights, const int *valid,
-                             const fm_expert_weights *shared, int shared_bits,
+                             const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
                              float shared_gate_score, uint32_t hidden, uint32_t inter,
                              uint32_t group_size, const float *x, const float *h_mid, float *out,
                              uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
@@ -871,14 +923,14 @@ extern "C" int fm_moe_decode(int K, const fm_expert_weights *experts, const int 
     a.h_mid = h_mid;
     a.out = out;
     a.out_bf16 = out_bf16;
-    return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
+    return fm_decode_launch_shared(a, shared_inter, ws, ws_bytes, fm_stream(stream));
 }
 
 // T tokens (rows of idx/weights/x/h_mid/out/out_bf16, entries of
 // shared_gate_score) in one launch; T > 1 only through fm_moe_decode_pool_tokens.
 static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int K, const int *idx,
                                const float *weights, const fm_expert_weights *shared, int shared_bits,
-                               const float *shared_gate_score, const float *x, const float *h_mid, float *out,
+                               uint32_t shared_inter, const float *shared_gate_score, const float *x, const float *h_mid, float *out,
                                uint16_t *out_bf16, const uint16_t *norm_w, float norm_eps, float *normed, void *ws,
                                size_t ws_bytes, void *stream, int T = 1) {
     FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
@@ -922,11 +974,13 @@ static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int 
     a.out = out;
     a.out_bf16 = out_bf16;
     if (T > 1) {
+        if (fm_shared_apart(K, a.has_shared, a.inter, shared_inter))
+            return fm_fail(FM_ERR_UNSUPPORTED, "%s: several tokens with a shared expert of its own size", who);
         a.ntok = T;
         a.spt = a.S;
         a.S = T * a.spt;
     }
-    return fm_decode_launch(a, ws, ws_bytes, fm_stream(stream));
+    return fm_decode_launch_shared(a, shared_inter, ws, ws_bytes, fm_stream(stream));
 }
 
 size_t fm_moe_decode_tokens_workspace_size(int T, int K, int has_shared, uint32_t hidden, uint32_t inter) {
@@ -937,16 +991,17 @@ int fm_moe_decode_pool_tokens(const fm_expert_pool *pool, int T, int K, const in
                               const fm_expert_weights *shared, int shared_bits, const float *shared_gate_scores,
                               const float *X, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
                               size_t ws_bytes, void *stream) {
-    return fm_decode_pool_impl("fm_prefill_moe", pool, K, idx, weights, shared, shared_bits, shared_gate_scores, X,
+    return fm_decode_pool_impl("fm_prefill_moe", pool, K, idx, weights, shared, shared_bits, 0, shared_gate_scores, X,
                                h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream, T);
 }
 
 extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
-                                  const fm_expert_weights *shared, int shared_bits, const float *shared_gate_score,
-                                  const float *x, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
-                                  size_t ws_bytes, void *stream) {
+                                  const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
+                                  const float *shared_gate_score, const float *x, const float *h_mid, float *out,
+                                  uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
     fm_clear_error();
-    return fm_decode_pool_impl("fm_moe_decode_pool", pool, K, idx, weights, shared, shared_bits, shared_gate_score, x,
+    return fm_decode_pool_impl("fm_moe_decode_pool", pool, K, idx, weights, shared, shared_bits, shared_inter,
+                               shared_gate_score, x,
                                h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream);
 }
 
@@ -989,14 +1044,15 @@ static int fm_noalloc_scratch(hipStream_t st, void **out) {
 extern "C" size_t fm_noalloc_workspace_bytes(void) { return FM_NOALLOC_WS_BYTES; }
 
 extern "C" int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
-                                          const fm_expert_weights *shared, int shared_bits,
+                                          const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
                                           const float *shared_gate_score, const float *x, const float *h_mid,
                                           float *out, uint16_t *out_bf16, void *stream) {
     const char *who = "fm_moe_decode_pool_noalloc";
     fm_clear_error();
     FM_REQUIRE(pool, "%s: NULL pool", who);
     FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
-    const size_t need = fm_moe_decode_workspace_size(K + (shared ? 1 : 0), pool->hidden, pool->inter);
+    const size_t need =
+        fm_moe_decode_workspace_size_ex(K, shared ? 1 : 0, pool->hidden, pool->inter, shared ? shared_inter : 0);
     if (need > FM_NOALLOC_WS_BYTES)
         return fm_fail(FM_ERR_UNSUPPORTED, "%s: K=%d, hidden %u, inter %u need a %zu-byte workspace; the static one "
                        "holds %zu bytes (use fm_moe_decode_pool with a caller workspace)", who, K, pool->hidden,
@@ -1004,19 +1060,19 @@ extern "C" int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, con
     void *ws = nullptr;
     const int rc = fm_noalloc_scratch(fm_stream(stream), &ws);
     if (rc) return rc;
-    return fm_decode_pool_impl(who, pool, K, idx, weights, shared, shared_bits, shared_gate_score, x, h_mid, out,
-                               out_bf16, nullptr, 0.f, nullptr, ws, FM_NOALLOC_WS_BYTES, stream);
+    return fm_decode_pool_impl(who, pool, K, idx, weights, shared, shared_bits, shared_inter, shared_gate_score, x,
+                               h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, FM_NOALLOC_WS_BYTES, stream);
 }
 
 extern "C" int fm_moe_decode_pool_norm(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
-                                       const fm_expert_weights *shared, int shared_bits,
+                                       const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
                                        const float *shared_gate_score, const float *x, const float *h_mid,
                                        float *out, uint16_t *out_bf16, const uint16_t *norm_w, float eps,
                                        float *normed, void *ws, size_t ws_bytes, void *stream) {
     fm_clear_error();
     FM_REQUIRE(norm_w && normed, "fm_moe_decode_pool_norm: NULL norm weights or output");
     FM_REQUIRE(eps >= 0.f, "fm_moe_decode_pool_norm: eps < 0");
-    return fm_decode_pool_impl("fm_moe_decode_pool_norm", pool, K, idx, weights, shared, shared_bits,
+    return fm_decode_pool_impl("fm_moe_decode_pool_norm", pool, K, idx, weights, shared, shared_bits, shared_inter,
                                shared_gate_score, x, h_mid, out, out_bf16, norm_w, eps, normed, ws, ws_bytes, stream);
 }
 

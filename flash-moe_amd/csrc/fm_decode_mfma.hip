@@ -600,7 +600,8 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             } while (++it < FM_SPIN_MAX);
             if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
             const float sw =
-                a.has_shared ? (a.shared_score ? fm_sigmoid(a.shared_score[tokB]) : a.shared_w_host) : 0.f;
+                (a.has_shared || a.shared_y) ? (a.shared_score ? fm_sigmoid(a.shared_score[tokB]) : a.shared_w_host)
+                                             : 0.f;
             const float yl = L.ylast[lane];
             float moe = 0.f;
 #pragma unroll
@@ -613,6 +614,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
             const size_t orow = (size_t)tokB * H + row;
             float o = a.h_mid ? __fadd_rn(a.h_mid[orow], moe) : moe;
             if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, yl));
+            else if (a.shared_y) o = __fadd_rn(o, __fmul_rn(sw, a.shared_y[orow]));
             a.out[orow] = o;
             if (a.out_bf16) a.out_bf16[orow] = fm_f32_to_bf16(o);
             if (a.norm_w) {

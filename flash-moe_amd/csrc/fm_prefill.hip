@@ -761,6 +761,12 @@ __global__ __launch_bounds__(256) void fm_pf_combine_kernel(const float *y, cons
     if (out_bf16) out_bf16[(size_t)t * H + i] = fm_f32_to_bf16(v);
 }
 
+// SwiGLU of the apart shared expert's gate and up rows, in place into g.
+__global__ __launch_bounds__(256) void fm_pf_swiglu_kernel(float *g, const float *u, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) g[i] = fm_silu_mul(g[i], u[i]);
+}
+
 // ---------------------------------------------------------------- host -----
 static uint32_t pf_max_chunks(int T, int K, uint32_t E, int has_shared) {
     // sum_e ceil(n_e / 64) <= min(E, T*K) + T*K / 64, plus the shared expert
@@ -798,9 +804,18 @@ static PfOps pf_ops_layout(size_t rows, uint32_t in_dim, bool lo, size_t o) {
 struct PfLayout {
     size_t entries, chunks, nchunks, err, gout, uout, y, total;
     PfOps xo, ao;
+    size_t sh_ws, sh_ws_bytes, sh_g, sh_u;  // shared expert of its own intermediate size (sh_ws_bytes > 0)
 };
 
-static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t inter, int has_shared) {
+// A shared expert whose intermediate size differs from the routed experts'
+// (config.h:23 shared_intermediate) runs apart, as three plain dequant GEMMs
+// over all tokens (as pfb_batched_shared_expert does, batched_prefill.h:122-226).
+static bool pf_shared_apart(int has_shared, uint32_t inter, uint32_t shared_inter) {
+    return has_shared && shared_inter != 0 && shared_inter != inter;
+}
+
+static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t inter, int has_shared,
+                          uint32_t shared_inter = 0) {
     PfLayout L;
     const size_t nent = (size_t)T * K + (has_shared ? T : 0);
     const uint32_t mc = pf_max_chunks(T, K, E, has_shared);
@@ -825,13 +840,23 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     o = L.xo.total;
     L.ao = pf_ops_layout(nent, inter, false, o);
     o = L.ao.total;
+    L.sh_ws = L.sh_ws_bytes = L.sh_g = L.sh_u = 0;
+    if (pf_shared_apart(has_shared, inter, shared_inter)) {
+        L.sh_ws = o;
+        L.sh_ws_bytes = fm_align_up(fm_pfb_gemm_workspace_size((uint32_t)T, hidden > shared_inter ? hidden : shared_inter), 256);
+        o += L.sh_ws_bytes;
+        L.sh_g = o;
+        o += fm_align_up((size_t)T * shared_inter * 4, 256);
+        L.sh_u = o;
+        o += fm_align_up((size_t)T * shared_inter * 4, 256);
+    }
     L.total = o;
     return L;
 }
 
-extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool) {
+extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool, uint32_t shared_inter) {
     if (!pool || T <= 0 || K <= 0) return 0;
-    return pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1).total;
+    return pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, 1, shared_inter).total;
 }
 
 static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,
@@ -895,7 +920,8 @@ static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
 }
 
 extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const int *idx, const float *weights,
-                              const fm_expert_weights *shared, int shared_bits, const float *shared_gate_scores,
+                              const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
+                              const float *shared_gate_scores,
                               const float *X, const float *h_mid, float *out, uint16_t *out_bf16, void *ws,
                               size_t ws_bytes, void *stream) {
     const char *who = "fm_prefill_moe";
@@ -910,14 +936,18 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
         FM_REQUIRE(shared_bits == 2 || shared_bits == 4, "%s: shared_bits must be 2 or 4", who);
     }
     const int has_shared = shared ? 1 : 0;
-    PfLayout L = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, has_shared);
+    if (shared_inter == pool->inter) shared_inter = 0;
+    if (has_shared && shared_inter)
+        FM_REQUIRE(shared_inter % 64 == 0 && shared_inter <= 16384, "%s: shared_inter %u", who, shared_inter);
+    const bool apart = pf_shared_apart(has_shared, pool->inter, shared_inter);
+    PfLayout L = pf_layout(T, K, pool->num_experts, pool->hidden, pool->inter, has_shared, shared_inter);
     if (!ws || ws_bytes < L.total)
         return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", who, ws_bytes, L.total);
     // A few tokens (batched decode): fused decode steps stream
     // each token's experts once at decode efficiency; the grouped GEMM only pays
     // off once experts are shared by many tokens.  Same result per token
     // (batched_prefill.h:241-308 is per-token decode arithmetic).
-    if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K) {
+    if (T <= FM_PREFILL_DECODE_MAX_T && K <= FM_MAX_K && !apart) {
         if (T > 1 && fm_moe_decode_tokens_workspace_size(T, K, has_shared, pool->hidden, pool->inter) <= ws_bytes) {
             // all tokens in one decode launch when the kernel takes T x (K + shared) slots
             const int rc = fm_moe_decode_pool_tokens(pool, T, K, idx, weights, shared, shared_bits,
@@ -930,7 +960,7 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
         if (dws <= ws_bytes) {
             for (int t = 0; t < T; t++) {
                 const int rc = fm_moe_decode_pool(pool, K, idx + (size_t)t * K, weights + (size_t)t * K, shared,
-                                                  shared_bits, shared_gate_scores ? shared_gate_scores + t : nullptr,
+                                                  shared_bits, 0, shared_gate_scores ? shared_gate_scores + t : nullptr,
                                                   X + (size_t)t * pool->hidden,
                                                   h_mid ? h_mid + (size_t)t * pool->hidden : nullptr,
                                                   out + (size_t)t * pool->hidden,
@@ -945,14 +975,16 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     char *p = (char *)ws;
     hipStream_t st = fm_stream(stream);
-    const uint32_t mc = pf_max_chunks(T, K, pool->num_experts, has_shared);
-    const size_t nent = (size_t)T * K + has_shared * T;
+    // the grouped GEMM takes the shared expert as one more expert unless it runs apart
+    const int grouped_shared = apart ? 0 : has_shared;
+    const uint32_t mc = pf_max_chunks(T, K, pool->num_experts, grouped_shared);
+    const size_t nent = (size_t)T * K + grouped_shared * T;
 
     // lists
     size_t lds = ((size_t)pool->num_experts * 3 + 5) * sizeof(int);
     if (lds > 65536) return fm_fail(FM_ERR_UNSUPPORTED, "%s: too many experts", who);
     hipLaunchKernelGGL(fm_pf_lists_kernel, dim3(1), dim3(1024), lds, st, idx, T, K, (int)pool->num_experts,
-                       has_shared, pool->blobs, pool->bits, shared ? shared_bits : 4, (int *)(p + L.entries),
+                       grouped_shared, pool->blobs, pool->bits, shared ? shared_bits : 4, (int *)(p + L.entries),
                        (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err));
     int rc = fm_check_launch("fm_pf_lists_kernel");
     if (rc) return rc;
@@ -1010,6 +1042,24 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     a.y = y;
     rc = pf_launch_gemm(a, false, st);
     if (rc) return rc;
+    if (apart) {
+        // shared expert over all tokens: gate, up (X -> [T][shared_inter]), SwiGLU, down into y rows T*K + t
+        float *g = (float *)(p + L.sh_g), *u = (float *)(p + L.sh_u);
+        void *gw = p + L.sh_ws;
+        rc = fm_pfb_gemm(shared->gate_w, shared->gate_s, shared->gate_b, X, g, (uint32_t)T, shared_inter,
+                         pool->hidden, 64, shared_bits, gw, L.sh_ws_bytes, stream);
+        if (!rc)
+            rc = fm_pfb_gemm(shared->up_w, shared->up_s, shared->up_b, X, u, (uint32_t)T, shared_inter,
+                             pool->hidden, 64, shared_bits, gw, L.sh_ws_bytes, stream);
+        if (rc) return rc;
+        const size_t n = (size_t)T * shared_inter;
+        hipLaunchKernelGGL(fm_pf_swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, n);
+        rc = fm_check_launch("fm_pf_swiglu_kernel");
+        if (!rc)
+            rc = fm_pfb_gemm(shared->down_w, shared->down_s, shared->down_b, g, y + (size_t)T * K * pool->hidden,
+                             (uint32_t)T, pool->hidden, shared_inter, 64, shared_bits, gw, L.sh_ws_bytes, stream);
+        if (rc) return rc;
+    }
     // combine
     dim3 cg((pool->hidden + 255) / 256, T);
     hipLaunchKernelGGL(fm_pf_combine_kernel, cg, dim3(256), 0, st, y, weights, T, K, (int)pool->hidden, has_shared,

@@ -52,7 +52,7 @@ class MoeLayer(ctypes.Structure):
                 ("seg_w", ctypes.c_void_p), ("seg_s", ctypes.c_void_p), ("seg_b", ctypes.c_void_p),
                 ("seg_bits", ctypes.c_int),
                 ("shared", ExpertWeights), ("shared_bits", ctypes.c_int), ("has_shared", ctypes.c_int),
-                ("pool", ExpertPool)]
+                ("pool", ExpertPool), ("shared_inter", ctypes.c_uint32)]
 
 
 class ExpertExtent(ctypes.Structure):
@@ -83,25 +83,26 @@ SIGNATURES = {
     "fm_dequant_matvec": (I32, [P, P, P, P, P, U32, U32, U32, I32, P]),
     "fm_batch_matvec": (I32, [P, U32, ctypes.POINTER(BatchMatvecSpec), I32, P]),
     "fm_moe_decode_workspace_size": (SZ, [I32, U32, U32]),
+    "fm_moe_decode_workspace_size_ex": (SZ, [I32, I32, U32, U32, U32]),
     "fm_encode_experts_batched": (I32, [I32, P, ctypes.POINTER(ExpertWeights), P, U32, U32, U32, P, P,
                                         P, SZ, P]),
     "fm_moe_combine": (I32, [P, P, P, P, I32, P, P, P, P, U32, P]),
     "fm_moe_decode": (I32, [I32, ctypes.POINTER(ExpertWeights), P, P, P, ctypes.POINTER(ExpertWeights),
-                            I32, F32, U32, U32, U32, P, P, P, P, P, SZ, P]),
+                            I32, U32, F32, U32, U32, U32, P, P, P, P, P, SZ, P]),
     "fm_moe_decode_pool": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
-                                 I32, P, P, P, P, P, P, SZ, P]),
+                                 I32, U32, P, P, P, P, P, P, SZ, P]),
     "fm_moe_decode_pool_norm": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
-                                      I32, P, P, P, P, P, P, F32, P, P, SZ, P]),
+                                      I32, U32, P, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),
     "fm_workspace_status": (I32, [P, ctypes.POINTER(ctypes.c_uint32), P]),
     "fm_noalloc_workspace_bytes": (ctypes.c_size_t, []),
     "fm_moe_decode_pool_noalloc": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
-                                         I32, P, P, P, P, P, P]),
+                                         I32, U32, P, P, P, P, P, P]),
     "fm_workspace_init": (I32, [P, ctypes.c_size_t, P]),
     "fm_route_topk": (I32, [P, I32, I32, I32, P, P, P]),
-    "fm_prefill_moe_workspace_size": (SZ, [I32, I32, ctypes.POINTER(ExpertPool)]),
+    "fm_prefill_moe_workspace_size": (SZ, [I32, I32, ctypes.POINTER(ExpertPool), U32]),
     "fm_prefill_moe": (I32, [ctypes.POINTER(ExpertPool), I32, I32, P, P, ctypes.POINTER(ExpertWeights),
-                             I32, P, P, P, P, P, P, SZ, P]),
+                             I32, U32, P, P, P, P, P, P, SZ, P]),
     "fm_pfb_gemm_workspace_size": (SZ, [U32, U32]),
     "fm_pfb_gemm": (I32, [P, P, P, P, P, U32, U32, U32, U32, I32, P, SZ, P]),
     "fm_moe_forward_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32]),

@@ -17,7 +17,7 @@ __all__ = [
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
     "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
     "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS", "STATUS_EPOCH_WRAP", "workspace_init",
-    "workspace", "moe_decode_pool_noalloc",
+    "workspace", "moe_decode_pool_noalloc", "decode_workspace_bytes_ex",
 ]
 
 STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP = 1, 2, 4, 8
@@ -65,6 +65,10 @@ def decode_workspace_bytes(n_slots, hidden, inter):
     return lib().fm_moe_decode_workspace_size(n_slots, hidden, inter)
 
 
+def decode_workspace_bytes_ex(K, has_shared, hidden, inter, shared_inter):
+    return lib().fm_moe_decode_workspace_size_ex(K, int(bool(has_shared)), hidden, inter, shared_inter)
+
+
 def _experts_array(experts):
     arr = (ExpertWeights * max(1, len(experts)))()
     for i, e in enumerate(experts):
@@ -73,40 +77,40 @@ def _experts_array(experts):
 
 
 def moe_decode(experts, bits, weights, x, out, ws, hidden, inter, valid=None, shared=None,
-               shared_bits=4, shared_score=0.0, h_mid=None, out_bf16=None, stream=None):
+               shared_bits=4, shared_score=0.0, h_mid=None, out_bf16=None, stream=None, shared_inter=0):
     K = len(experts)
     check(lib().fm_moe_decode(
         K, _experts_array(experts), _i32_array(bits), _f32_array(weights),
         _i32_array(valid) if valid is not None else None,
-        ctypes.byref(shared) if shared is not None else None, shared_bits, float(shared_score),
+        ctypes.byref(shared) if shared is not None else None, shared_bits, shared_inter, float(shared_score),
         hidden, inter, 64, ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws), ws.numel() * ws.element_size(),
         stream_ptr(stream)))
 
 
 def moe_decode_pool(pool, idx, weights, x, out, ws, shared=None, shared_bits=4, shared_score=None,
-                    h_mid=None, out_bf16=None, stream=None):
+                    h_mid=None, out_bf16=None, stream=None, shared_inter=0):
     K = idx.numel()
     check(lib().fm_moe_decode_pool(
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
-        shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
+        shared_bits, shared_inter, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
         ws.numel() * ws.element_size(), stream_ptr(stream)))
 
 
 def moe_decode_pool_noalloc(pool, idx, weights, x, out, shared=None, shared_bits=4, shared_score=None,
-                            h_mid=None, out_bf16=None, stream=None):
+                            h_mid=None, out_bf16=None, stream=None, shared_inter=0):
     """fm_moe_decode_pool on the library's static per-GPU workspace (no allocation)."""
     K = idx.numel()
     check(lib().fm_moe_decode_pool_noalloc(
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
-        shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), stream_ptr(stream)))
+        shared_bits, shared_inter, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), stream_ptr(stream)))
 
 
 def moe_decode_pool_norm(pool, idx, weights, x, out, ws, norm_w, eps, normed, shared=None, shared_bits=4,
-                         shared_score=None, h_mid=None, out_bf16=None, stream=None):
+                         shared_score=None, h_mid=None, out_bf16=None, stream=None, shared_inter=0):
     K = idx.numel()
     check(lib().fm_moe_decode_pool_norm(
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
-        shared_bits, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(norm_w), float(eps),
+        shared_bits, shared_inter, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(norm_w), float(eps),
         ptr(normed), ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
 
 
@@ -153,16 +157,16 @@ def route_topk(logits, K, idx, weights, stream=None):
     check(lib().fm_route_topk(ptr(logits), T, E, K, ptr(idx), ptr(weights), stream_ptr(stream)))
 
 
-def prefill_workspace_bytes(T, K, pool):
-    return lib().fm_prefill_moe_workspace_size(T, K, ctypes.byref(pool.c))
+def prefill_workspace_bytes(T, K, pool, shared_inter=0):
+    return lib().fm_prefill_moe_workspace_size(T, K, ctypes.byref(pool.c), shared_inter)
 
 
 def prefill_moe(pool, idx, weights, X, out, ws, shared=None, shared_bits=4, shared_scores=None, h_mid=None,
-                out_bf16=None, stream=None):
+                out_bf16=None, stream=None, shared_inter=0):
     T, K = idx.shape
     check(lib().fm_prefill_moe(
         ctypes.byref(pool.c), T, K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
-        shared_bits, ptr(shared_scores), ptr(X), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
+        shared_bits, shared_inter, ptr(shared_scores), ptr(X), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
         ws.numel() * ws.element_size(), stream_ptr(stream)))
 
 

@@ -27,7 +27,7 @@ size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K) {
     n += align256(sizeof(float));                                      /* seg score */
     n += align256((size_t)K * sizeof(int));                            /* idx */
     n += align256((size_t)K * sizeof(float));                          /* weights */
-    n += fm_moe_decode_workspace_size(K + 1, L->pool.hidden, L->pool.inter);
+    n += fm_moe_decode_workspace_size_ex(K, L->has_shared, L->pool.hidden, L->pool.inter, L->shared_inter);
     return n;
 }
 
@@ -40,7 +40,8 @@ static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const
     size_t need = fm_moe_forward_workspace_size(L, K);
     if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_forward: workspace too small");
     /* [decode step's workspace: status word first][logits][seg][idx][w] */
-    const size_t step = fm_moe_decode_workspace_size(K + 1, L->pool.hidden, L->pool.inter);
+    const size_t step =
+        fm_moe_decode_workspace_size_ex(K, L->has_shared, L->pool.hidden, L->pool.inter, L->shared_inter);
     char *p = (char *)ws + step;
     float *logits = (float *)p;
     p += align256((size_t)L->pool.num_experts * sizeof(float));
@@ -67,10 +68,10 @@ static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const
      * layer's input RMS norm (3995-4029) */
     if (norm_w)
         return fm_moe_decode_pool_norm(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL, L->shared_bits,
-                                       L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16, norm_w, eps,
+                                       L->shared_inter, L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16, norm_w, eps,
                                        normed, p, rest, stream);
     return fm_moe_decode_pool(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL,
-                              L->shared_bits, L->has_shared ? seg : NULL, h_post, h_mid, out,
+                              L->shared_bits, L->shared_inter, L->has_shared ? seg : NULL, h_post, h_mid, out,
                               out_bf16, p, rest, stream);
 }
 
@@ -97,7 +98,7 @@ size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {
     /* the expert step's region (its header and decode-tagged words first) and
      * the router GEMM's region are disjoint: the GEMM never overwrites tags */
     n += align256(fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden));
-    return n + align256(fm_prefill_moe_workspace_size(T, K, &L->pool));
+    return n + align256(fm_prefill_moe_workspace_size(T, K, &L->pool, L->shared_inter));
 }
 
 int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_post,
@@ -108,7 +109,7 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     size_t need = fm_moe_prefill_workspace_size(L, K, T);
     if (!ws || ws_bytes < need) return fm_host_fail(FM_ERR_WORKSPACE, "fm_moe_prefill_forward: workspace too small");
     /* [expert step region: header first][router GEMM region][logits][seg][idx][w] */
-    const size_t step = align256(fm_prefill_moe_workspace_size(T, K, &L->pool));
+    const size_t step = align256(fm_prefill_moe_workspace_size(T, K, &L->pool, L->shared_inter));
     const size_t gemm = align256(fm_pfb_gemm_workspace_size((uint32_t)T, L->pool.hidden));
     char *g = (char *)ws + step;
     char *p = g + gemm;
@@ -136,6 +137,6 @@ int fm_moe_prefill_forward(const fm_moe_layer *L, int K, int T, const float *h_p
     rc = fm_route_topk(logits, T, (int)L->pool.num_experts, K, idx, w, stream);
     if (rc) return rc;
     return fm_prefill_moe(&L->pool, T, K, idx, w, L->has_shared ? &L->shared : NULL,
-                          L->shared_bits, L->has_shared ? seg : NULL, h_post, h_mid, out,
+                          L->shared_bits, L->shared_inter, L->has_shared ? seg : NULL, h_post, h_mid, out,
                           out_bf16, p, rest, stream);
 }

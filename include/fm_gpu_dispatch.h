@@ -130,6 +130,13 @@ int fm_batch_matvec(const float *x, uint32_t x_dim, const fm_batch_matvec_spec *
  * calls need their own. */
 size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter);
 
+/* Workspace bytes for a decode step of K routed experts (+ the shared expert
+ * when has_shared) whose shared expert has its own intermediate size
+ * shared_inter (config.h:23 shared_intermediate; 0 = inter).  Equal sizes give
+ * fm_moe_decode_workspace_size(K + has_shared, ...). */
+size_t fm_moe_decode_workspace_size_ex(int K, int has_shared, uint32_t hidden, uint32_t inter,
+                                       uint32_t shared_inter);
+
 /* Zero a decode / prefill / layer workspace (ws_bytes rounded down to 16 B)
  * with a kernel on `stream` (no hipMemsetAsync: recordable into a graph). */
 int fm_workspace_init(void *ws, size_t ws_bytes, void *stream);
@@ -170,14 +177,18 @@ int fm_moe_combine(const float *h_mid, const float *expert_outs, const float *we
 
 /* The fused decode step (CMD3 of layer_forward.h:3895-3993): K routed experts
  * and the shared expert, gate/up/SwiGLU/down, weighted accumulation and the
- * residual, in two kernel launches.
+ * residual, in one kernel launch.  shared_inter is the shared expert's own
+ * intermediate size (config.h:23 shared_intermediate, layer_forward.h:
+ * 1099-1137; 0 = inter); when it differs from inter the shared expert runs
+ * as a second, one-slot launch before the step (workspace:
+ * fm_moe_decode_workspace_size_ex).
  *   out = h_mid + sum_k weights[k]*E_k(x) + sigmoid(shared_gate_score)*S(x)
  * experts/bits/weights/valid are HOST arrays [K] (K <= FM_MAX_K, routing done
  * on the CPU as in layer_forward.h:3519-3523); valid may be NULL.  shared may
  * be NULL (no shared term).  h_mid and out_bf16 may be NULL. */
 int fm_moe_decode(int K, const fm_expert_weights *experts, const int *bits,
                   const float *weights, const int *valid,
-                  const fm_expert_weights *shared, int shared_bits,
+                  const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
                   float shared_gate_score, uint32_t hidden, uint32_t inter,
                   uint32_t group_size, const float *x, const float *h_mid,
                   float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
@@ -185,11 +196,11 @@ int fm_moe_decode(int K, const fm_expert_weights *experts, const int *bits,
 
 /* Same step with routing on the device: idx/weights are DEVICE arrays [K]
  * (e.g. from fm_route_topk), experts come from `pool`, shared_gate_score is a
- * device scalar (may be NULL: weight 1 for the shared expert is NOT implied;
- * NULL drops the sigmoid and uses weight 1.0f).  No host synchronisation. */
+ * device scalar; NULL means the shared expert enters with weight 1.0f (no
+ * sigmoid).  shared_inter as for fm_moe_decode.  No host synchronisation. */
 int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
                        const float *weights, const fm_expert_weights *shared,
-                       int shared_bits, const float *shared_gate_score,
+                       int shared_bits, uint32_t shared_inter, const float *shared_gate_score,
                        const float *x, const float *h_mid, float *out,
                        uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
 
@@ -207,7 +218,7 @@ int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
 size_t fm_noalloc_workspace_bytes(void);
 int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx,
                                const float *weights, const fm_expert_weights *shared,
-                               int shared_bits, const float *shared_gate_score,
+                               int shared_bits, uint32_t shared_inter, const float *shared_gate_score,
                                const float *x, const float *h_mid, float *out,
                                uint16_t *out_bf16, void *stream);
 
@@ -219,7 +230,7 @@ int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx
  * combine where the fused kernel runs, otherwise one extra launch. */
 int fm_moe_decode_pool_norm(const fm_expert_pool *pool, int K, const int *idx,
                             const float *weights, const fm_expert_weights *shared,
-                            int shared_bits, const float *shared_gate_score,
+                            int shared_bits, uint32_t shared_inter, const float *shared_gate_score,
                             const float *x, const float *h_mid, float *out,
                             uint16_t *out_bf16, const uint16_t *norm_w, float eps,
                             float *normed, void *ws, size_t ws_bytes, void *stream);
@@ -246,8 +257,9 @@ int fm_route_topk(const float *logits, int T, int E, int K, int *idx, float *wei
 /* Prefill                                                                   */
 /* ------------------------------------------------------------------------ */
 
-/* Workspace bytes for fm_prefill_moe with T tokens, K routed per token. */
-size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool);
+/* Workspace bytes for fm_prefill_moe with T tokens, K routed per token and a
+ * shared expert of intermediate size shared_inter (0 = pool->inter). */
+size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool, uint32_t shared_inter);
 
 /* Batched-prefill MoE layer as a per-expert grouped dequant-GEMM on MFMA.
  * Same result as the per-token loop of batched_prefill.h:241-308 plus the
@@ -260,10 +272,12 @@ size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_pool *pool);
  * Up to 8 tokens (K <= 16, hidden 4096 / inter 1024) run as ONE launch of
  * the decode kernel over all T x (K + shared) slots (batched decode: few
  * experts are shared, so grouping buys nothing); bit-equal to
- * fm_moe_decode_pool per token. */
+ * fm_moe_decode_pool per token.  A shared expert whose shared_inter differs
+ * from pool->inter (0 = same) runs apart as three plain dequant GEMMs over all
+ * tokens, as pfb_batched_shared_expert does (batched_prefill.h:122-226). */
 int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const int *idx,
                    const float *weights, const fm_expert_weights *shared, int shared_bits,
-                   const float *shared_gate_scores, const float *X, const float *h_mid,
+                   uint32_t shared_inter, const float *shared_gate_scores, const float *X, const float *h_mid,
                    float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
                    void *stream);
 

@@ -25,6 +25,8 @@ typedef struct {
     int shared_bits;
     int has_shared;
     fm_expert_pool pool;                        /* routed experts (packed blobs)         */
+    uint32_t shared_inter;                      /* shared_expert_intermediate_size (config.h:23,200);
+                                                   0 = the routed experts' pool.inter       */
 } fm_moe_layer;
 
 size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K);

@@ -261,7 +261,7 @@ void fmo_expert_forward(const uint8_t *blob, int bits, int hidden, int inter,
  */
 void fmo_moe_decode(int K, const uint8_t *const *blobs, const int *bits,
                     const float *w, const int *valid,
-                    const uint8_t *shared_blob, int shared_bits, float shared_gate_score,
+                    const uint8_t *shared_blob, int shared_bits, int shared_inter, float shared_gate_score,
                     int hidden, int inter, int group_size,
                     const float *x, const float *h_mid, float *out) {
     float *moe = (float *)calloc((size_t)hidden, sizeof(float));
@@ -273,7 +273,7 @@ void fmo_moe_decode(int K, const uint8_t *const *blobs, const int *bits,
         fmo_vec_madd(moe, eo, w[k], hidden);
     }
     if (shared_blob) {
-        fmo_expert_forward(shared_blob, shared_bits, hidden, inter, group_size, x, so);
+        fmo_expert_forward(shared_blob, shared_bits, hidden, shared_inter ? shared_inter : inter, group_size, x, so);
         float sw = fmo_sigmoid(shared_gate_score);
         for (int i = 0; i < hidden; i++) so[i] *= sw;
     }
@@ -290,7 +290,7 @@ void fmo_moe_decode(int K, const uint8_t *const *blobs, const int *bits,
  */
 void fmo_prefill_moe(int T, int K, const int *idx, const float *w,
                      const uint8_t *const *blob_table, const int *bits_table,
-                     const uint8_t *shared_blob, int shared_bits,
+                     const uint8_t *shared_blob, int shared_bits, int shared_inter,
                      const float *shared_gate_scores,
                      int hidden, int inter, int group_size,
                      const float *X, const float *h_mid, float *out) {
@@ -307,7 +307,7 @@ void fmo_prefill_moe(int T, int K, const int *idx, const float *w,
         }
         float sw = 0.0f;
         if (shared_blob) {
-            fmo_expert_forward(shared_blob, shared_bits, hidden, inter, group_size, x, so);
+            fmo_expert_forward(shared_blob, shared_bits, hidden, shared_inter ? shared_inter : inter, group_size, x, so);
             sw = fmo_sigmoid(shared_gate_scores ? shared_gate_scores[t] : 0.0f);
         }
         float *o = out + (size_t)t * hidden;

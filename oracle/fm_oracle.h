@@ -72,10 +72,12 @@ void fmo_expert_forward(const uint8_t *blob, int bits, int hidden, int inter,
 /* layer_forward.h:1143-1305 routed + shared combine (CPU path):
  *   moe = sum_k w_k * expert_k(x)        (cpu_vec_madd, slot order, skipped if !valid)
  *   out = h_mid + moe + sigmoid(shared_gate_score) * shared(x)
- * blobs[k] / bits[k] for the K routed experts; shared_blob may be NULL. */
+ * blobs[k] / bits[k] for the K routed experts; shared_blob may be NULL.  The
+ * shared expert has its own intermediate size shared_inter (config.h:23,
+ * layer_forward.h:1099-1137; 0 = inter). */
 void fmo_moe_decode(int K, const uint8_t *const *blobs, const int *bits,
                     const float *w, const int *valid,
-                    const uint8_t *shared_blob, int shared_bits, float shared_gate_score,
+                    const uint8_t *shared_blob, int shared_bits, int shared_inter, float shared_gate_score,
                     int hidden, int inter, int group_size,
                     const float *x, const float *h_mid, float *out);
 
@@ -83,7 +85,7 @@ void fmo_moe_decode(int K, const uint8_t *const *blobs, const int *bits,
  * idx/w are [T,K]; blob_table[e] / bits_table[e] the expert pool. */
 void fmo_prefill_moe(int T, int K, const int *idx, const float *w,
                      const uint8_t *const *blob_table, const int *bits_table,
-                     const uint8_t *shared_blob, int shared_bits,
+                     const uint8_t *shared_blob, int shared_bits, int shared_inter,
                      const float *shared_gate_scores,
                      int hidden, int inter, int group_size,
                      const float *X, const float *h_mid, float *out);

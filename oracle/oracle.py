@@ -52,8 +52,8 @@ class OracleLib:
             "fmo_route": (None, [_P, _I, _I, _P, _P, _P]),
             "fmo_expert_offsets": (ctypes.c_size_t, [_I, _I, _I, _I, _P]),
             "fmo_expert_forward": (None, [_P, _I, _I, _I, _I, _P, _P]),
-            "fmo_moe_decode": (None, [_I, _P, _P, _P, _P, _P, _I, _F, _I, _I, _I, _P, _P, _P]),
-            "fmo_prefill_moe": (None, [_I, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P]),
+            "fmo_moe_decode": (None, [_I, _P, _P, _P, _P, _P, _I, _I, _F, _I, _I, _I, _P, _P, _P]),
+            "fmo_prefill_moe": (None, [_I, _I, _P, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P]),
             "fmo_dequant_gemm": (None, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
         }
         for n, (r, a) in sig.items():
@@ -147,7 +147,7 @@ class OracleLib:
         return out
 
     def moe_decode(self, blobs, bits, w, x, hidden, inter, valid=None, shared_blob=None, shared_bits=4,
-                   shared_score=0.0, h_mid=None, group_size=64):
+                   shared_score=0.0, h_mid=None, group_size=64, shared_inter=0):
         K = len(blobs)
         blobs = [_c(b, np.uint8) for b in blobs]
         ptrs = (ctypes.c_void_p * max(1, K))(*[b.ctypes.data for b in blobs])
@@ -159,11 +159,11 @@ class OracleLib:
         hm = None if h_mid is None else _c(h_mid, np.float32)
         out = np.empty(hidden, dtype=np.float32)
         self.L.fmo_moe_decode(K, ctypes.cast(ptrs, _P), _p(bits_a), _p(w_a), _p(valid_a), _p(sb), shared_bits,
-                              float(shared_score), hidden, inter, group_size, _p(x), _p(hm), _p(out))
+                              shared_inter, float(shared_score), hidden, inter, group_size, _p(x), _p(hm), _p(out))
         return out
 
     def prefill_moe(self, idx, w, blob_table, bits_table, X, hidden, inter, shared_blob=None, shared_bits=4,
-                    shared_scores=None, h_mid=None, group_size=64):
+                    shared_scores=None, h_mid=None, group_size=64, shared_inter=0):
         idx, w = _c(idx, np.int32), _c(w, np.float32)
         T, K = idx.shape
         blob_table = [_c(b, np.uint8) if b is not None else None for b in blob_table]
@@ -175,7 +175,7 @@ class OracleLib:
         hm = None if h_mid is None else _c(h_mid, np.float32)
         out = np.empty((T, hidden), dtype=np.float32)
         self.L.fmo_prefill_moe(T, K, _p(idx), _p(w), ctypes.cast(ptrs, _P), _p(bits_a), _p(sb), shared_bits,
-                               _p(ss), hidden, inter, group_size, _p(X), _p(hm), _p(out))
+                               shared_inter, _p(ss), hidden, inter, group_size, _p(X), _p(hm), _p(out))
         return out
 
 

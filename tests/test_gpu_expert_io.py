@@ -75,7 +75,7 @@ def test_load_layer_prefill(orc, dev, tiered_model):
         rng = synth.rng_for(22)
         idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
         X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
-        ws = fm.workspace(fm.lib().fm_prefill_moe_workspace_size(Tn, K, lp.c), dev)
+        ws = fm.workspace(fm.lib().fm_prefill_moe_workspace_size(Tn, K, lp.c, 0), dev)
         out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
         fm.prefill_moe(lp, T(idx, dev), T(w, dev), T(X, dev), out, ws)
         torch.cuda.synchronize()

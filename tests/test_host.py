@@ -79,7 +79,7 @@ def test_argument_validation_without_gpu():
     rc = L.fm_route_topk(fake, 1, 512, 65, fake, fake, None)
     assert rc == -1 and b"K=65" in L.fm_last_error()
     # decode: K too large, then a workspace that is too small
-    rc = L.fm_moe_decode(17, None, None, None, None, None, 4, 0.0, 4096, 1024, 64, fake, None, fake, None,
+    rc = L.fm_moe_decode(17, None, None, None, None, None, 4, 0, 0.0, 4096, 1024, 64, fake, None, fake, None,
                          None, 0, None)
     assert rc == -1
     experts = (fmoe_amd.ExpertWeights * 1)()
@@ -87,7 +87,7 @@ def test_argument_validation_without_gpu():
         setattr(experts[0], f, 1 << 20)
     bits = (ctypes.c_int * 1)(4)
     w = (ctypes.c_float * 1)(1.0)
-    rc = L.fm_moe_decode(1, experts, bits, w, None, None, 4, 0.0, 4096, 1024, 64, fake, None, fake, None, fake,
+    rc = L.fm_moe_decode(1, experts, bits, w, None, None, 4, 0, 0.0, 4096, 1024, 64, fake, None, fake, None, fake,
                          16, None)
     assert rc == -2 and b"workspace" in L.fm_last_error()
     need = L.fm_moe_decode_workspace_size(11, 4096, 1024)
@@ -140,7 +140,7 @@ def test_prefill_workspace_covers_few_token_decode():
     L.fm_moe_decode_workspace_size.restype = ctypes.c_size_t
     for T in range(1, 10):
         for K in (1, 4, 10, 16):
-            pf = L.fm_prefill_moe_workspace_size(T, K, ctypes.byref(pool))
+            pf = L.fm_prefill_moe_workspace_size(T, K, ctypes.byref(pool), 0)
             need = L.fm_moe_decode_workspace_size(T * (K + 1), 4096, 1024)
             # hand-off buffers: 8-byte tagged words per activation and per output row
             assert need >= T * (K + 1) * (1024 + 4096) * 8

@@ -374,3 +374,29 @@ def test_f32_to_bf16_rne_vs_float64_brute(orc):
     low = u[(u & 0xFFFF) < 0x8000]
     for v in low[:2000].view(np.float32):
         assert orc.L.fmo_f32_to_bf16_rne(float(v)) == orc.L.fmo_f32_to_bf16_trunc(float(v))
+
+
+def test_shared_expert_own_intermediate_size(orc):
+    # layer_forward.h:1099-1137 sizes the shared expert by cfg.shared_intermediate:
+    # with no routed experts the step is h_mid + sigmoid(g) * shared(x) at that size
+    rng = synth.rng_for(32)
+    H, Is = 1024, 768
+    sb = synth.expert_blob((32, 1), H, Is, 4)
+    x = synth.hidden_vec(rng, H)
+    hm = rng.normal(0, 1, H).astype(np.float32)
+    got = orc.moe_decode([], [], np.zeros(0, np.float32), x, H, 512, shared_blob=sb, shared_bits=4,
+                         shared_score=0.3, h_mid=hm, shared_inter=Is)
+    so = orc.expert_forward(sb, 4, H, Is, x)
+    want = hm + np.float32(orc.sigmoid(0.3)) * so
+    assert norm_err(got, want) < 1e-6
+    # prefill per token agrees with decode per token at the shared expert's own size
+    blobs = [synth.expert_blob((32, 10 + e), H, 512, 4) for e in range(4)]
+    idx, w = orc.route(rng.normal(0, 1, (3, 4)).astype(np.float32), 2)
+    X = synth.hidden_vec(rng, H, (3, H))
+    g = rng.normal(0, 1, 3).astype(np.float32)
+    P = orc.prefill_moe(idx, w, blobs, [4] * 4, X, H, 512, shared_blob=sb, shared_bits=4, shared_scores=g,
+                        shared_inter=Is)
+    for t in range(3):
+        d = orc.moe_decode([blobs[e] for e in idx[t]], [4, 4], w[t], X[t], H, 512, shared_blob=sb, shared_bits=4,
+                           shared_score=float(g[t]), shared_inter=Is)
+        assert norm_err(P[t], d) < 1e-6

@@ -69,6 +69,6 @@ def test_noalloc_rejects_oversized_shape():
     assert fm.lib().fm_noalloc_workspace_bytes() == 2 << 20
     dummy = (ctypes.c_void_p * 1)(1)
     pool = fm.ExpertPool(ctypes.cast(dummy, ctypes.c_void_p).value, 1, 1, 16384, 4096, 64)
-    rc = fm.lib().fm_moe_decode_pool_noalloc(ctypes.byref(pool), 16, 1, 1, None, 4, None, 1, None, 1, None, None)
+    rc = fm.lib().fm_moe_decode_pool_noalloc(ctypes.byref(pool), 16, 1, 1, None, 4, 0, None, 1, None, 1, None, None)
     assert rc == -4  # FM_ERR_UNSUPPORTED
     assert "static one holds" in fm.lib().fm_last_error().decode()
