@@ -140,3 +140,56 @@ def test_stage_invalid_expert_is_skipped(orc, dev, tmp_path):
     torch.cuda.synchronize()
     ref = orc.moe_decode([blobs[e] for e in ids], [4] * K, w, x, HIDDEN, INTER, valid=valid)
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_deferred_decode_overlaps_next_staging(orc, dev, tiered_model):
+    """Deferred completion (layer_forward.h:1587-1602, 1658, 4033): the decode of
+    token t is enqueued and NOT waited for; the expert I/O of token t+1 (preads
+    + host->device copies on a second stream) runs meanwhile; then both are
+    joined and checked -- decode t against the oracle, token t+1's staged bytes
+    byte-exact.  Two slot-buffer sets alternate so staging never overwrites
+    what an in-flight decode reads."""
+    import torch
+    d, m = tiered_model
+    K, NT, layer = 8, 4, 0
+    slot = fm.layout_of(HIDDEN, INTER, 64, 4).size
+    sets = [torch.zeros((K, slot), dtype=torch.uint8, device=dev) for _ in range(2)]
+    s_dec, s_io = torch.cuda.Stream(), torch.cuda.Stream()
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
+    torch.cuda.synchronize()
+    rng = synth.rng_for(25)
+    ids = [[int(e) for e in rng.permutation(E)[:K]] for _ in range(NT)]
+    xs = [synth.hidden_vec(rng, HIDDEN) for _ in range(NT)]
+    ws_k = [rng.dirichlet(np.ones(K)).astype(np.float32) for _ in range(NT)]
+    outs = [torch.empty(HIDDEN, dtype=torch.float32, device=dev) for _ in range(NT)]
+    dec_done = [None] * NT
+    with ExpertStore(d, 2, E, HIDDEN, INTER, io_threads=4) as st:
+        st.stage(layer, ids[0], [sets[0][k].data_ptr() for k in range(K)], stream=s_io)
+        staged = torch.cuda.Event()
+        staged.record(s_io)
+        for t in range(NT):
+            say("deferred token", t)
+            bl = [m[layer][e][1] for e in ids[t]]
+            ex = [fm.experts_from_blob(sets[t % 2][k], bl[k], HIDDEN, INTER) for k in range(K)]
+            s_dec.wait_event(staged)  # token t's experts are in HBM
+            fm.moe_decode(ex, bl, ws_k[t], T(xs[t], dev), outs[t], ws, HIDDEN, INTER, stream=s_dec)
+            dec_done[t] = torch.cuda.Event()
+            dec_done[t].record(s_dec)
+            if t + 1 < NT:  # next token's I/O while the decode may still run
+                if t >= 1:
+                    s_io.wait_event(dec_done[t - 1])  # that set was read by decode t-1
+                st.stage_start(layer, ids[t + 1], [sets[(t + 1) % 2][k].data_ptr() for k in range(K)], stream=s_io)
+                loaded, valid = st.stage_wait()
+                assert loaded == K and valid == [1] * K
+                staged = torch.cuda.Event()
+                staged.record(s_io)
+            # complete_deferred_experts: join, then check both results
+            dec_done[t].synchronize()
+            ref = orc.moe_decode([m[layer][e][0] for e in ids[t]], bl, ws_k[t], xs[t], HIDDEN, INTER)
+            assert norm_err(outs[t].cpu().numpy(), ref) <= TOL_F32, t
+            if t + 1 < NT:
+                staged.synchronize()
+                got = sets[(t + 1) % 2].cpu().numpy()
+                for k, e in enumerate(ids[t + 1]):
+                    assert np.array_equal(got[k, : m[layer][e][0].size], m[layer][e][0]), (t + 1, k)
+    assert fm.workspace_status(ws) == 0

@@ -146,3 +146,20 @@ def test_prefill_workspace_covers_few_token_decode():
             assert need >= T * (K + 1) * (1024 + 4096) * 8
             if T <= 8:
                 assert pf >= need, (T, K)
+
+
+def test_c_consumer_compiles_and_links(tmp_path):
+    """A C program that includes only include/*.h (and the HIP runtime API) and
+    links -lfmoe with --no-undefined: every entry point it calls resolves in
+    libfmoe.so.  Run without arguments it stops before any GPU call."""
+    import subprocess
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    exe = tmp_path / "fm_consumer"
+    cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Werror", f"-I{root}/include", "-I/opt/rocm/include",
+           "-D__HIP_PLATFORM_AMD__", os.path.join(here, "c_consumer", "fm_consumer.c"), "-o", str(exe),
+           f"-L{root}/flash-moe_amd/lib", "-lfmoe", f"-Wl,-rpath,{root}/flash-moe_amd/lib", "-L/opt/rocm/lib",
+           "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined"]
+    subprocess.run(cmd, check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
