@@ -366,3 +366,36 @@ def test_workspace_status_bad_expert(orc, dev, pool64):
     ref = orc.moe_decode([blobs[3], blobs[11]], [bits[3], bits[11]], w[[0, 2]], x, HIDDEN, INTER)
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
     assert fm.workspace_status(ws) == 0  # cleared by the previous read
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_unpacked_codes_bit_exact_one_hot(orc, dev, bits):
+    """With a one-hot x the dequant product is exactly one code:
+    out[r] = c[r,i] * s + b, and c * s is exact in fp32, so the GPU result must
+    equal the oracle's bit for bit -- for every field position of a packed word
+    (all 64 positions of one group, plus a few in other groups).  Checked
+    through the matvec kernel and the MFMA GEMM (one token per position)."""
+    import torch
+    say("one-hot codes", bits)
+    out_dim, in_dim = 96, 512
+    W, s, b = matrix(700 + bits, out_dim, in_dim, bits)
+    pos = list(range(64, 128)) + [0, 7, 200, 333, 511]
+    X = np.zeros((len(pos), in_dim), np.float32)
+    for t, i in enumerate(pos):
+        X[t, i] = 1.0
+    Y = torch.empty((len(pos), out_dim), dtype=torch.float32, device=dev)
+    ws = torch.empty(fm.lib().fm_pfb_gemm_workspace_size(len(pos), in_dim), dtype=torch.uint8, device=dev)
+    fm.pfb_gemm(T(W, dev), T(s, dev), T(b, dev), T(X, dev), Y, bits, ws)
+    out = torch.empty((len(pos), out_dim), dtype=torch.float32, device=dev)
+    dW, ds, db = T(W, dev), T(s, dev), T(b, dev)
+    for t in range(len(pos)):
+        fm.dequant_matvec(dW, ds, db, T(X[t], dev), out[t], bits)
+    torch.cuda.synchronize()
+    ref = orc.gemm(bits, W, s, b, X)
+    # the oracle itself: c * s + b of the unpacked code, element by element
+    codes = orc.unpack(bits, W).reshape(out_dim, in_dim).astype(np.float32)
+    sf, bf = synth.bf16_to_f32(s), synth.bf16_to_f32(b)
+    want = np.stack([codes[:, i] * sf[:, i // 64] + bf[:, i // 64] for i in pos]).astype(np.float32)
+    assert np.array_equal(ref.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(Y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
