@@ -56,6 +56,36 @@ def pmc_traffic(name):
     return round(d["fetch_kib"] * 1024 * d["fetch_scale"] + d["write_kib"] * 1024 * d["write_scale"])
 
 
+def graph_of(step, items):
+    """step(i) for every i in items recorded into one HIP graph (on a side
+    stream, as stream capture requires).  Replaying it runs exactly those
+    kernels with no host work between them, as a serving loop would."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in items:
+                step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, n):
+    """ms per step of a graph of n steps, HIP events around one replay."""
+    import torch
+    g.replay()  # first replay uploads the graph
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
 def bench_decode(args, dev):
     import numpy as np
     import torch
@@ -88,6 +118,7 @@ def bench_decode(args, dev):
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    # eager: one Python call per launch (host-bound at these kernel times)
     t0 = time.perf_counter()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -96,7 +127,16 @@ def bench_decode(args, dev):
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    step_ms = e0.elapsed_time(e1) / args.steps
+    eager_ms = e0.elapsed_time(e1) / args.steps
+    # the timed steps: routing + fused step of every token, recorded into one
+    # HIP graph (the kernels keep their hand-off tag on the device, so replays
+    # are valid) and replayed back to back
+    g = graph_of(step, range(args.warmup, nsteps))
+    step_ms = time_graph(g, args.steps)
+    status = fm.workspace_status(ws)
+    if status:
+        raise SystemExit(f"decode workspace status {status}: a step's output is invalid")
+    del g
     # algorithmic bytes per step: K routed + shared blobs, x, h_mid, out fp32 + bf16
     blob = fm.layout_of(H, I, 64, 4).size
     step_bytes = (K + 1) * blob + H * 4 * 3 + H * 2 + E * 4
@@ -104,24 +144,24 @@ def bench_decode(args, dev):
     # done above for every step) between two events on its stream
     torch.cuda.synchronize()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record()
-    for i in range(args.warmup, nsteps):
+
+    def dec(i):
         fm.moe_decode_pool(pool, idx[i], w[i], x, out, ws, shared=shared[i % n_sh], shared_bits=4,
                            shared_score=scores[i:i + 1], h_mid=hm, out_bf16=ob)
-    k1.record()
-    torch.cuda.synchronize()
-    kern_ms = k0.elapsed_time(k1) / args.steps
+
+    g = graph_of(dec, range(args.warmup, nsteps))
+    kern_ms = time_graph(g, args.steps)
+    del g
     # the same launches with the next layer's input RMS norm fused into the combine
     nw = torch.from_numpy(synth.bf16_bits(rng.normal(1, 0.1, H).astype(np.float32)).view(np.int16)).to(dev)
     normed = torch.empty(H, dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
-    k0.record()
-    for i in range(args.warmup, nsteps):
+    def dec_norm(i):
         fm.moe_decode_pool_norm(pool, idx[i], w[i], x, out, ws, nw, 1e-6, normed, shared=shared[i % n_sh],
                                 shared_bits=4, shared_score=scores[i:i + 1], h_mid=hm, out_bf16=ob)
-    k1.record()
-    torch.cuda.synchronize()
-    norm_ms = k0.elapsed_time(k1) / args.steps
+
+    g = graph_of(dec_norm, range(args.warmup, nsteps))
+    norm_ms = time_graph(g, args.steps)
+    del g
     # the whole MoE block of one decode token through the C layer driver
     # (fm_moe_forward): router + shared-gate matvecs, routing, fused experts
     Wr, sr, br = synth.quant_matrix(synth.rng_for(3010), E, H, 4)
@@ -137,23 +177,21 @@ def bench_decode(args, dev):
     Lr.pool = pool.c
     lws = fm.workspace(fm.moe_forward_workspace_bytes(Lr, K), dev)
     hps = torch.from_numpy(synth.hidden_vec(rng, H, (16, H))).to(dev)
+    def layer(i):
+        Lr.shared = shared[i % n_sh]
+        fm.moe_forward(Lr, K, hps[i % 16], hm, out, lws, out_bf16=ob)
+
     for i in range(args.warmup):
-        Lr.shared = shared[i % n_sh]
-        fm.moe_forward(Lr, K, hps[i % 16], hm, out, lws, out_bf16=ob)
-    torch.cuda.synchronize()
-    k0.record()
-    for i in range(args.steps):
-        Lr.shared = shared[i % n_sh]
-        fm.moe_forward(Lr, K, hps[i % 16], hm, out, lws, out_bf16=ob)
-    k1.record()
-    torch.cuda.synchronize()
-    layer_ms = k0.elapsed_time(k1) / args.steps
+        layer(i)
+    g = graph_of(layer, range(args.steps))
+    layer_ms = time_graph(g, args.steps)
+    del g
     router_bytes = E * H // 2 + E * (H // 64) * 4 + H // 2 + (H // 64) * 4
     kern_bytes = (K + 1) * blob + H * 4 * 3 + H * 2
     # unique experts actually touched per step (routing may repeat across steps, never within)
     achieved = kern_bytes / (kern_ms * 1e-3) / 1e9
     res = {
-        "step_ms": step_ms, "wall_s": wall, "step_bytes": step_bytes,
+        "step_ms": step_ms, "wall_s": wall, "step_bytes": step_bytes, "eager_us_per_step": round(eager_ms * 1e3, 2),
         "value": step_bytes / (step_ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": pmc_traffic("decode_config2_pmc.json"),
@@ -260,14 +298,9 @@ def bench_tiered(args, dev):
 
         for i in range(args.warmup):
             step(i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(args.warmup, n):
-            step(i)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
+        g = graph_of(step, range(args.warmup, n))
+        ms = time_graph(g, args.steps)
+        del g
         ids = idx[args.warmup:].cpu().numpy()
         nbytes = []
         for i in range(args.steps):
@@ -304,24 +337,18 @@ def bench_small(args, dev, pool):
     # launches outpace the GPU (a Python wrapper per call would not)
     import ctypes
     L = fm.lib()
-    sp = fm.stream_ptr()
     mv_args = [(c[0].data_ptr(), c[1].data_ptr(), c[2].data_ptr()) for c in copies]
     xp, yp = x.data_ptr(), y.data_ptr()
 
     def mv(i):
         w_, s_, b_ = mv_args[i % n]
-        return L.fm_dequant_matvec(w_, s_, b_, xp, yp, 4096, 4096, 64, 4, sp)
+        return L.fm_dequant_matvec(w_, s_, b_, xp, yp, 4096, 4096, 64, 4, fm.stream_ptr())
 
     for i in range(10):
         fm.check(mv(i))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps):
-        mv(i)
-    e1.record()
-    torch.cuda.synchronize()
-    mv_us = e0.elapsed_time(e1) * 1e3 / steps
+    g = graph_of(mv, range(steps))
+    mv_us = time_graph(g, steps) * 1e3
+    del g
     mv_bytes = 4096 * 512 * 4 + 2 * 4096 * 64 * 2 + 4096 * 2 + 4096 * 4
     ws = fm.workspace(fm.decode_workspace_bytes(1, H, I), dev)
     out = torch.empty(H, dtype=torch.float32, device=dev)
@@ -333,18 +360,14 @@ def bench_small(args, dev, pool):
     wsp, wsb, outp = ws.data_ptr(), ws.numel(), out.data_ptr()
 
     def ex(i):
-        return L.fm_moe_decode(1, ex_args[(i * 37) % E], bits1, w1, None, None, 4, 0.0, H, I, 64, xp, None, outp,
-                               None, wsp, wsb, sp)
+        return L.fm_moe_decode(1, ex_args[(i * 37) % E], bits1, w1, None, None, 4, 0, 0.0, H, I, 64, xp, None, outp,
+                               None, wsp, wsb, fm.stream_ptr())
 
     for i in range(10):
         fm.check(ex(i))
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(steps):
-        ex(i)
-    e1.record()
-    torch.cuda.synchronize()
-    ex_us = e0.elapsed_time(e1) * 1e3 / steps
+    g = graph_of(ex, range(steps))
+    ex_us = time_graph(g, steps) * 1e3
+    del g
     ex_bytes = fm.layout_of(H, I, 64, 4).size + H * 2 + H * 4
     return {"config0_matvec": {"workload": "4096x4096 4-bit g64 matvec, 32 rotating copies", "us": round(mv_us, 2),
                                "bytes": mv_bytes, "gbs": round(mv_bytes / mv_us / 1e3, 1),
@@ -517,7 +540,10 @@ def main():
         "hbm_frac": dec["value"] / HBM_PEAK_GBS,
         "config": {"workload": "config 2: MoE decode b=1, 512 experts, top-10 + shared, "
                                "4096->1024->4096 SwiGLU, 4-bit g64, device routing",
-                   "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"]},
+                   "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"],
+                   "timing": "the K timed steps (routing + fused step each) recorded into one HIP graph, "
+                             "replayed once between HIP events",
+                   "eager_us_per_step": dec["eager_us_per_step"]},
         "roofline": dec["roofline"],
         "layer_step": dec["layer_step"],
         "single": small,
