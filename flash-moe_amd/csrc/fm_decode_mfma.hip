@@ -34,6 +34,8 @@
 // the wave's own gate/up work is done.
 #include "fm_decode.h"
 
+#include <stdlib.h>
+
 typedef _Float16 fmm_h8 __attribute__((ext_vector_type(8)));
 typedef float fmm_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t fmm_u2 __attribute__((ext_vector_type(2)));
@@ -159,6 +161,42 @@ FM_DEV float fmm_row_sum(float v) {
 struct FmmCodes {
     fm_u4 c[8];
 };
+
+// The code loads of fmm_issue alone (scales and biases loaded elsewhere),
+// issued on every path: with !ok every lane reads the first 256 bytes of
+// `dummy` instead, so the number of loads in flight never depends on a branch
+// (the compiler's wait counts stay exact instead of falling back to "wait for
+// everything").  bits must be 2 or 4 either way.
+FM_DEV void fmm_issue_codes(const uint32_t *W, int bits, uint32_t row0, uint32_t in_dim, uint32_t g0, bool ok,
+                            FmmCodes &cd, int lane, const void *dummy) {
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t G = in_dim / 64, wpg = 2 * bits, wpr = ok ? G * wpg : 0;
+    if (!ok) {
+        W = (const uint32_t *)dummy;
+        row0 = g0 = 0;
+    }
+    // always 8 loads: a 2-bit row piece is 4 of them, its other 4 repeat the
+    // same addresses (cache hits) so the load count never depends on bits
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t row = row0 + 4 * j + kq;
+            const uint32_t po = (ok && bits == 4) ? g0 * wpg + 64 * p : (ok ? g0 * wpg : 0);
+            cd.c[4 * p + j] = fm_ldg_u4_nt(W + (size_t)row * wpr + po + 4 * n);
+        }
+    }
+}
+
+// The scale / bias runs of fmm_issue (lane (n, kq): row row0 + n, groups
+// g0 + 4 kq .. + 3), branch-free like fmm_issue_codes.
+FM_DEV void fmm_issue_sb(const uint16_t *S, const uint16_t *B, uint32_t row0, uint32_t in_dim, uint32_t g0, bool ok,
+                         fmm_u2 &sc, fmm_u2 &bi, int lane, const void *dummy) {
+    const int n = lane & 15, kq = lane >> 4;
+    const size_t o = ok ? (size_t)(row0 + n) * (in_dim / 64) + g0 + 4 * kq : 0;
+    sc = *(const FM_GLOBAL fmm_u2 *)(ok ? S + o : (const uint16_t *)dummy);
+    bi = *(const FM_GLOBAL fmm_u2 *)(ok ? B + o : (const uint16_t *)dummy);
+}
 
 // Issue the loads of 16 rows x 16 groups (groups g0 .. g0+15) of one matrix.
 // Load j of piece p: lane l reads row row0 + 4j + l/16, words 64p + 4(l%16)
@@ -647,6 +685,396 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     }
 }
 
+// ------------------------------------------------ one workgroup per CU ----
+// The single-token step with ONE 768-thread workgroup per CU holding up to
+// three work items (item = A tile + B tile of one slot, as above; item i of
+// workgroup g is g + i * grid).  A CU's vector memory requests are served in
+// issue order, so one workgroup per CU decides that order itself:
+//   x (once per CU, not once per item), then every item's gate/up rows, then
+//   every item's down rows -- all issued before any compute.
+// The gate/up bytes thus arrive first everywhere, the activations they feed
+// are published while the down bytes are still streaming, and the last bytes
+// a CU receives are down rows whose activations are (mostly) ready: the tail
+// after the stream is one hand-off plus the combine.  Slot descriptors come
+// from wave-uniform scalar loads (idx -> pool tables), which do not queue
+// behind the vector stream.  The four waves of an item synchronise through an
+// LDS counter, so items progress independently of each other.
+#define FMC_NG 3                  // items per workgroup
+#define FMC_THREADS (256 * FMC_NG)
+
+struct __attribute__((aligned(16))) FmcItem {
+    fm_h2 aq[2][FMM_GI][32];      // the item's activations as MFMA operand rows
+    float asum[FMM_GI];
+    float ainv[FMM_GI];
+    float act[FMM_MAXI];          // staged activations (fp32)
+    float part[4][16][2];         // per-wave partial gate/up sums
+    float ylast[64];              // combine: this item's rows of the last slot's y
+    uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
+    uint32_t scl[4][16][FMM_GH / 2];  // gate/up scales and biases of the 16 rows (bf16 pairs)
+    float cw[FM_MAX_SLOTS];       // combine: every slot's weight
+    uint32_t cvalid;              // combine: bit k = slot k is valid
+    uint32_t sync;                // the item's 4-wave barrier counter
+};
+
+struct __attribute__((aligned(16))) FmcLds {
+    fm_h2 xq[2][FMM_GH][32];
+    fm_h2 zero[32];
+    float xsum[FMM_GH];
+    float xinv[FMM_GH];
+    uint32_t xready;              // count of item 0's waves that built the x operands
+    FmcItem it[FMC_NG];
+};
+
+typedef __attribute__((address_space(4))) const uint32_t fmc_cu32;
+typedef __attribute__((address_space(4))) const uint64_t fmc_cu64;
+// Loads through the constant address space: wave-uniform addresses become
+// scalar loads (memory written by earlier launches only).
+FM_DEV uint32_t fmc_ld32(const void *p) { return *(fmc_cu32 *)p; }
+FM_DEV uint64_t fmc_ld64(const void *p) { return *(fmc_cu64 *)p; }
+
+// Slot k (wave-uniform) resolved with scalar loads: idx / weight, then the
+// pool's blob address and bit width.
+FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k) {
+    if (!a.pool_mode || k >= a.K) return a.slot[k];
+    FmSlot s;
+    const int e = (int)fmc_ld32(a.idx + k);
+    const float w = __uint_as_float(fmc_ld32(a.wdev + k));
+    if (e < 0 || (uint32_t)e >= a.pool_n) {
+        s.valid = 0;
+        s.bits = 4;
+        s.weight = 0.f;
+        return s;
+    }
+    const char *blob = (const char *)fmc_ld64(a.pool_blobs + e);
+    const uintptr_t bp = (uintptr_t)(a.pool_bits + e);
+    const int bits = (int)((fmc_ld32((const void *)(bp & ~(uintptr_t)3)) >> (8 * (bp & 3))) & 0xffu);
+    const uint64_t *off = bits == 2 ? a.off2 : a.off4;
+    s.gw = (const uint32_t *)(blob + off[0]);
+    s.gs = (const uint16_t *)(blob + off[1]);
+    s.gb = (const uint16_t *)(blob + off[2]);
+    s.uw = (const uint32_t *)(blob + off[3]);
+    s.us = (const uint16_t *)(blob + off[4]);
+    s.ub = (const uint16_t *)(blob + off[5]);
+    s.dw = (const uint32_t *)(blob + off[6]);
+    s.ds = (const uint16_t *)(blob + off[7]);
+    s.db = (const uint16_t *)(blob + off[8]);
+    s.bits = bits;
+    s.weight = w;
+    s.valid = blob != nullptr && (bits == 2 || bits == 4);
+    return s;
+}
+
+// Barrier of the 4 waves of one item: an LDS counter that only grows (target
+// += 4 per use).  Waits on LDS operations only -- the item's weight loads stay
+// in flight across it.
+FM_DEV void fmc_item_sync(uint32_t *ctr, uint32_t &target) {
+    target += 4;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+        __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeArgs a) {
+    __shared__ FmcLds L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = __builtin_amdgcn_readfirstlane(tid >> 8);  // the wave's item
+    const int wv = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
+    const int gt = tid & 255;  // thread within the item
+    const int n = lane & 15, q = lane >> 4;
+    constexpr uint32_t H = FMM_H, I = FMM_MAXI, GI = FMM_MAXI / 64, TILES = FMM_H / 64;  // == I / 16
+    const uint32_t item = blockIdx.x + gridDim.x * (uint32_t)grp;
+    const bool has = item < (uint32_t)a.S * TILES;
+    const int k = has ? (int)(item / TILES) : 0;  // the item's slot
+    const uint32_t tile = item % TILES;
+
+    FM_DX_MARK(0);
+    // counters first (no load is in flight yet, so this barrier is cheap)
+    if (tid < FMC_NG) L.it[tid].sync = 0;
+    if (tid == 0) L.xready = 0;
+    __syncthreads();
+    const uint32_t ep_ld = fm_epoch_load(a);
+    // x: every wave loads elements 16 t .. 16 t + 15 of its item-relative
+    // thread t (items 1 and 2 hit the lines item 0 brings into the CU's
+    // cache); item 0 turns them into operand rows below
+    fm_f4 xr[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * gt + 4 * j);
+    const FmSlot s = fmc_slot(a, k);
+    const bool doA = has && s.valid;
+    // Every gate/up load of the item.  Loads issue in order and block while
+    // the CU's request queue is full, so a wave issues its down rows only
+    // after its activations are published (a blocked issue would hold back
+    // the gate/up compute behind it).
+    const uint32_t rowA0 = tile * 16, rowB0 = tile * 64 + 16 * wv;
+    FmmCodes cg, cu, cdn;
+    fmm_u2 sdn = {0, 0}, bdn = {0, 0}, scl[4] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+    const int bits = doA ? s.bits : 4;
+    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * wv, doA, cg, lane, a.x);
+    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * wv, doA, cu, lane, a.x);
+    // the tile's gate/up scales and biases: 16 rows x 64 groups = 2 KB per
+    // array, contiguous; wave wv loads rows 4 wv .. 4 wv + 3 of each (full
+    // lines) and the item shares them through LDS
+    {
+        const uint16_t *arr[4] = {s.gs, s.gb, s.us, s.ub};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            scl[j] = *(const FM_GLOBAL fmm_u2 *)(doA ? arr[j] + (size_t)(rowA0 + 4 * wv) * FMM_GH + 4 * lane
+                                                       : (const uint16_t *)a.x);
+    }
+    FM_DX_MARK(1);
+    const bool last = has && a.mode == 0 && k == a.S - 1;
+    if (last && wv == 0) {
+        // the combine's slot weights, fetched now (scalar loads) so that the
+        // combine itself waits for nothing but the other slots' outputs
+        uint32_t vm = 0;
+#pragma unroll
+        for (int kk = 0; kk < FM_MAX_SLOTS; kk++) {
+            if (kk < a.S) {
+                const FmSlot sk = fmc_slot(a, kk);
+                if (lane == 0) L.it[grp].cw[kk] = sk.weight;
+                vm |= sk.valid ? 1u << kk : 0u;
+            }
+        }
+        if (lane == 0) L.it[grp].cvalid = vm;
+    }
+    // item 0 turns x into MFMA operand rows (both layouts), group sums and
+    // scales; the other items wait for them on an LDS flag, not a barrier
+    if (grp == 0) {
+        if (tid < 32) L.zero[tid] = fm_as_h2(0u);
+        const int g = tid >> 2, qq = tid & 3;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[4 * j] = xr[j].x;
+            v[4 * j + 1] = xr[j].y;
+            v[4 * j + 2] = xr[j].z;
+            v[4 * j + 3] = xr[j].w;
+        }
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float m = (j & 1) ? 0.0625f * f : f;
+                L.xq[0][g][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+            }
+        const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+        for (int n2 = 0; n2 < 8; n2++)
+            L.xq[1][g][8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
+        float sm = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if (qq == 0) {
+            L.xsum[g] = sm;
+            L.xinv[g] = fm_exp2i(24 - ex);
+        }
+    }
+    {
+        uint32_t xr_target = 0;
+        if (grp == 0) {
+            fmc_item_sync(&L.xready, xr_target);  // item 0's 4 waves have written the operands
+        } else {
+            while (__hip_atomic_load(&L.xready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 4)
+                __builtin_amdgcn_s_sleep(1);
+            asm volatile("" ::: "memory");
+        }
+    }
+    const uint32_t ep = fm_epoch_tag(ep_ld);
+    FmcItem &T = L.it[grp];
+    uint32_t phase = 0;
+    FM_DX_MARK(2);
+
+    // ---- A: gate/up partials of 16 rows over this wave's 16 groups ----
+    if (doA) {
+        fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
+        const fm_h2 *xq = &L.xq[s.bits == 4 ? 0 : 1][16 * wv][0];
+        if (s.bits == 4) {
+            fmm_mma<4>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
+            fmm_mma<4>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
+        } else {
+            fmm_mma<2>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
+            fmm_mma<2>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(fmm_u2 *)&T.scl[j][4 * wv + (lane >> 4)][2 * (lane & 15)] = scl[j];
+        fmc_item_sync(&T.sync, phase);
+        // lane (row n, q) folds groups 16 wv + 4 q .. + 3 of row n
+        const int c0 = 8 * wv + 2 * q;
+        const fmm_u2 sg = *(const fmm_u2 *)&T.scl[0][n][c0], bg = *(const fmm_u2 *)&T.scl[1][n][c0];
+        const fmm_u2 su = *(const fmm_u2 *)&T.scl[2][n][c0], bu = *(const fmm_u2 *)&T.scl[3][n][c0];
+        const float *gs4 = &L.xsum[16 * wv + 4 * q], *gi4 = &L.xinv[16 * wv + 4 * q];
+        float pg = fmm_fold(g0 + g1, sg, bg, gs4, gi4);
+        float pu = fmm_fold(u0 + u1, su, bu, gs4, gi4);
+        pg = fmm_q_sum(pg);
+        pu = fmm_q_sum(pu);
+        if (lane < 16) {
+            T.part[wv][n][0] = pg;
+            T.part[wv][n][1] = pu;
+        }
+    }
+    FM_DX_MARK(3);
+    fmc_item_sync(&T.sync, phase);
+    if (doA && gt < 16) {
+        const float g = (T.part[0][gt][0] + T.part[1][gt][0]) + (T.part[2][gt][0] + T.part[3][gt][0]);
+        const float u = (T.part[0][gt][1] + T.part[1][gt][1]) + (T.part[2][gt][1] + T.part[3][gt][1]);
+        fm_put_tagged(&a.act2[(size_t)k * I + rowA0 + gt], fm_silu_mul(g, u), ep);
+    }
+    // the down rows (queue behind every gate/up request of the CU)
+    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
+    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
+    FM_DX_MARK(4);
+
+    // ---- B: the slot's activations (every A tile of the slot), then 16 down rows per wave ----
+    if (doA) {
+        constexpr int MAXQ = FMM_MAXI / 256;
+        uint64_t t[MAXQ];
+        const uint64_t *src = a.act2 + (size_t)k * I;
+#pragma unroll
+        for (int j = 0; j < MAXQ; j++) t[j] = fm_get_tagged(src + j * 256 + gt);
+        uint32_t it = 0;
+        do {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < MAXQ; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+            if (__all(ready)) break;
+#pragma unroll
+            for (int j = 0; j < MAXQ; j++)
+                if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(src + j * 256 + gt);
+        } while (++it < FM_SPIN_MAX);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+#pragma unroll
+        for (int j = 0; j < MAXQ; j++) T.act[j * 256 + gt] = __uint_as_float((uint32_t)t[j]);
+    }
+    fmc_item_sync(&T.sync, phase);
+    if (doA) {
+        // per group (16 threads x 4 elements): sum, operand scale 2^e, operand rows
+        const int lay = s.bits == 4 ? 0 : 1;
+        const uint32_t g = gt >> 4;
+        const float *ag = T.act + 64 * g + 4 * (gt & 15);
+        float sm = (ag[0] + ag[1]) + (ag[2] + ag[3]);
+        float mx = fmaxf(fmaxf(fabsf(ag[0]), fabsf(ag[1])), fmaxf(fabsf(ag[2]), fabsf(ag[3])));
+        sm = fmm_row_sum(sm);
+        mx = fm_row16_max(mx);
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
+        if ((gt & 15) == 0) {
+            T.asum[g] = sm;
+            T.ainv[g] = fm_exp2i(24 - ex);
+        }
+        fmm_build_pair(T.act + 64 * g, s.bits, 2 * (gt & 15), f, &T.aq[lay][g][0]);
+        fmm_build_pair(T.act + 64 * g, s.bits, 2 * (gt & 15) + 1, f, &T.aq[lay][g][0]);
+    }
+    fmc_item_sync(&T.sync, phase);
+    FM_DX_MARK(5);
+    if (doA) {
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        const fm_h2 *aq = &T.aq[s.bits == 4 ? 0 : 1][0][0];
+        if (s.bits == 4)
+            fmm_mma<4>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+        else
+            fmm_mma<2>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+        float y = fmm_fold(d0 + d1, sdn, bdn, &T.asum[4 * q], &T.ainv[4 * q]);
+        y = fmm_q_sum(y);
+        const uint32_t row = rowB0 + n;
+        if (lane < 16) {
+            if (a.mode == 1)
+                a.expert_out[(size_t)k * H + row] = y;
+            else if (!last)
+                fm_put_tagged(&a.y2[(size_t)k * H + row], y, ep);
+            else
+                T.ylast[16 * wv + n] = y;
+        }
+    } else if (last && lane < 16) {
+        T.ylast[16 * wv + n] = 0.f;
+    }
+    FM_DX_MARK(6);
+
+    // ---- C: the items of the last slot combine their 64 rows over every slot ----
+    if (last) {
+        fmc_item_sync(&T.sync, phase);
+        if (wv == 0) {
+            const uint32_t row = tile * 64 + lane;
+            const int spt = a.S;
+            // every slot's weight and validity, fetched at the start
+            const uint32_t cv = T.cvalid;
+            uint64_t t[FM_MAX_SLOTS - 1];
+#pragma unroll
+            for (int kk = 0; kk < FM_MAX_SLOTS - 1; kk++)
+                t[kk] = (kk < spt - 1 && ((cv >> kk) & 1u)) ? fm_get_tagged(&a.y2[(size_t)kk * H + row])
+                                                            : ((uint64_t)ep << 32);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int kk = 0; kk < FM_MAX_SLOTS - 1; kk++) ready &= (uint32_t)(t[kk] >> 32) == ep;
+                if (__all(ready)) break;
+#pragma unroll
+                for (int kk = 0; kk < FM_MAX_SLOTS - 1; kk++)
+                    if ((uint32_t)(t[kk] >> 32) != ep) t[kk] = fm_get_tagged(&a.y2[(size_t)kk * H + row]);
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+            const float sw = (a.has_shared || a.shared_y)
+                                 ? (a.shared_score ? fm_sigmoid(a.shared_score[0]) : a.shared_w_host)
+                                 : 0.f;
+            const float yl = T.ylast[lane];
+            float moe = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < FM_MAX_SLOTS; kk++) {
+                if (kk < a.K && ((cv >> kk) & 1u)) {
+                    const float yk =
+                        kk == spt - 1 ? yl : __uint_as_float((uint32_t)t[kk < FM_MAX_SLOTS - 1 ? kk : 0]);
+                    moe = __fadd_rn(moe, __fmul_rn(T.cw[kk], yk));
+                }
+            }
+            float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+            if (a.has_shared) o = __fadd_rn(o, __fmul_rn(sw, yl));
+            else if (a.shared_y) o = __fadd_rn(o, __fmul_rn(sw, a.shared_y[row]));
+            a.out[row] = o;
+            if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+            if (a.norm_w) {
+                // next layer's input RMS norm (cpu_kernels.h:235-246): every
+                // combining item publishes the sum of squares of its 64 rows,
+                // then reduces all of them in the same fixed order
+                const float sq =
+                    __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(o * o))));
+                if (lane == 0) fm_put_tagged(&a.ss2[tile], sq, ep);
+                uint64_t v = lane < (int)TILES ? fm_get_tagged(&a.ss2[lane]) : ((uint64_t)ep << 32);
+                uint32_t it2 = 0;
+                while (!__all((uint32_t)(v >> 32) == ep) && ++it2 < FM_SPIN_MAX) {
+                    if ((uint32_t)(v >> 32) != ep) v = fm_get_tagged(&a.ss2[lane]);
+                }
+                if (it2 >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+                const float part = lane < (int)TILES ? __uint_as_float((uint32_t)v) : 0.f;
+                const float tot =
+                    __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(part))));
+                const float inv = 1.0f / sqrtf(tot / (float)H + a.norm_eps);
+                a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
+            }
+        }
+    }
+    FM_DX_MARK(7);
+    if (a.pool_mode && blockIdx.x == 0 && tid < a.K) {
+        const int e = a.idx[tid];
+        if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+    }
+    // the ends of the hand-off chains: combining items (mode 0) or every down
+    // item (mode 1) count towards publishing the next epoch
+    if (gt == 0 && has && (a.mode == 0 ? last : true))
+        fm_epoch_finish(a, ep, (a.mode == 0 ? 1u : (uint32_t)a.S) * TILES);
+}
+
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
     if (a.hidden != FMM_H || a.inter != FMM_MAXI)
@@ -663,6 +1091,20 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
+    static int per_cu_c = -1;
+    if (per_cu_c < 0 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel, FMC_THREADS, 0) != hipSuccess)
+        per_cu_c = 0;
+    const int cus = fm_num_cus();
+    // one token whose items fit three per CU: the one-workgroup-per-CU kernel
+    // (FMOE_DECODE_NO_CU set in the environment: the three-workgroup kernel,
+    // which tests compare it with)
+    const char *no_cu = getenv("FMOE_DECODE_NO_CU");
+    if (a.ntok <= 1 && per_cu_c >= 1 && (uint32_t)a.S * (FMM_H / 64) <= (uint32_t)(FMC_NG * cus) &&
+        a.S <= FM_MAX_SLOTS && !(no_cu && *no_cu)) {
+        hipLaunchKernelGGL(fm_decode_cu_kernel, dim3(cus), dim3(FMC_THREADS), 0, st, a);
+        return fm_check_launch("fm_decode_cu_kernel");
+    }
     const uint32_t tiles = a.inter / 16 > a.hidden / 64 ? a.inter / 16 : a.hidden / 64;
     const uint32_t items = (uint32_t)a.S * tiles;
     // every block may wait on others: the grid must be resident, and it is a

@@ -399,3 +399,41 @@ def test_unpacked_codes_bit_exact_one_hot(orc, dev, bits):
     assert np.array_equal(ref.view(np.uint32), want.view(np.uint32))
     assert np.array_equal(Y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("kernel", ["cu", "three_per_cu"])
+def test_decode_pool_both_mfma_kernels(orc, dev, pool64, kernel, monkeypatch):
+    """The one-workgroup-per-CU decode kernel and the three-workgroups-per-CU one
+    (FMOE_DECODE_NO_CU) on the same step, each against the oracle, with the
+    fused next-layer norm and a tiered pool."""
+    import torch
+    say("decode kernel", kernel)
+    if kernel == "three_per_cu":
+        monkeypatch.setenv("FMOE_DECODE_NO_CU", "1")
+    blobs, bits, pool = pool64
+    K = 10
+    rng = synth.rng_for(15, kernel == "cu")
+    lg = rng.normal(0, 1, (1, 64)).astype(np.float32)
+    x = synth.hidden_vec(rng, HIDDEN)
+    hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+    nw = synth.bf16_bits(rng.normal(1, 0.2, HIDDEN).astype(np.float32))
+    shared_blob = synth.expert_blob((4000, 3), HIDDEN, INTER, 2)
+    dsh = T(shared_blob, dev)
+    sh = fm.experts_from_blob(dsh, 2, HIDDEN, INTER)
+    idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+    w = torch.empty((1, K), dtype=torch.float32, device=dev)
+    fm.route_topk(T(lg, dev), K, idx, w)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    normed = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    g = T(np.array([-0.4], np.float32), dev)
+    for rep in range(3):
+        fm.moe_decode_pool_norm(pool, idx, w, T(x, dev), out, ws, T(nw.view(np.int16), dev), 1e-6, normed, shared=sh,
+                                shared_bits=2, shared_score=g, h_mid=T(hm, dev))
+    torch.cuda.synchronize()
+    ri, rw = orc.route(lg, K)
+    ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                         shared_blob=shared_blob, shared_bits=2, shared_score=-0.4, h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
+    assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, nw, 1e-6)) <= TOL_F32
+    assert fm.workspace_status(ws) == 0
