@@ -434,9 +434,28 @@ def bench_staging(args, dev):
             "bound": "host pread + PCIe host->device copy"}
 
 
-def cpu_baseline(sample_blobs, budget_s=10.0):
-    """The reference's own CPU kernels (oracle/_ref: cpu_dequant_matvec +
-    cpu_swiglu + cpu_vec_madd, one core) on config-2 steps until ~budget_s."""
+def host_info():
+    """CPU model and the cores this process may use (the box's host, not the GPU)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count()}
+
+
+def cpu_baseline(budget_s=10.0):
+    """The reference's own CPU path (oracle/_ref: cpu_dequant_matvec, cpu_swiglu,
+    cpu_vec_madd compiled from cpu_kernels.h; one core, as the reference runs
+    it) on bounded samples of configs 0-4.  Weights rotate over ~700 MB of
+    distinct blobs so the host's last-level cache cannot hold them.  Config 4's
+    2-bit experts use this build's C port (the reference has no CPU 2-bit kernel:
+    its CPU fallback misreads 2-bit blobs with the 4-bit kernel,
+    layer_forward.h:4106-4129)."""
     import numpy as np
     from fmoe_amd import synth
     from fmoe_amd.layout import expert_offsets
@@ -449,36 +468,94 @@ def cpu_baseline(sample_blobs, budget_s=10.0):
         kind = "port"
     from oracle import OracleLib
     O = OracleLib()
-    off, size = expert_offsets(H, I, 64, 4)
+    per = budget_s / 5.0
+    t_gen = time.perf_counter()
+    NB = 96
+    blobs4 = [synth.expert_blob((3400, e), H, I, 4) for e in range(NB)]
+    blobs2 = [synth.expert_blob((3401, e), H, I, 2) for e in range(48)]
+    gen_s = time.perf_counter() - t_gen
+    off4, size4 = expert_offsets(H, I, 64, 4)
+    size2 = expert_offsets(H, I, 64, 2)[1]
     x = synth.hidden_vec(synth.rng_for(5), H)
 
     def mats(blob, name, rows, cols):
-        w = blob[off[name + "_w"]: off[name + "_w"] + rows * cols // 2].view(np.uint32).reshape(rows, cols // 8)
-        s = blob[off[name + "_s"]: off[name + "_s"] + rows * cols // 32].view(np.uint16).reshape(rows, -1)
-        b = blob[off[name + "_b"]: off[name + "_b"] + rows * cols // 32].view(np.uint16).reshape(rows, -1)
+        w = blob[off4[name + "_w"]: off4[name + "_w"] + rows * cols // 2].view(np.uint32).reshape(rows, cols // 8)
+        s = blob[off4[name + "_s"]: off4[name + "_s"] + rows * cols // 32].view(np.uint16).reshape(rows, -1)
+        b = blob[off4[name + "_b"]: off4[name + "_b"] + rows * cols // 32].view(np.uint16).reshape(rows, -1)
         return w, s, b
 
-    def expert(blob):
-        if R is None:
-            return O.expert_forward(blob, 4, H, I, x)
-        g = R.matvec4(*mats(blob, "gate", I, H), x)
-        u = R.matvec4(*mats(blob, "up", I, H), x)
+    def expert(blob, bits, xin):
+        if R is None or bits == 2:
+            return O.expert_forward(blob, bits, H, I, xin)
+        g = R.matvec4(*mats(blob, "gate", I, H), xin)
+        u = R.matvec4(*mats(blob, "up", I, H), xin)
         return R.matvec4(*mats(blob, "down", H, I), R.swiglu(g, u))
 
-    steps, t0 = 0, time.perf_counter()
-    while True:
+    def madd(acc, e, w):
+        return R.vec_madd(acc, e, w) if R is not None else acc + np.float32(w) * e
+
+    def timed(fn):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn(n)
+            n += 1
+            if time.perf_counter() - t0 > per:
+                return n, time.perf_counter() - t0
+
+    res = {}
+    # config 0: 4096 x 4096 matvec; W views into the blob bytes (any byte is a
+    # valid pair of codes), real scales/biases
+    big = np.concatenate(blobs4[:40])
+    _, s0, b0 = synth.quant_matrix(synth.rng_for(3402), 4096, 4096, 4)
+    mv_w = 4096 * 512 * 4
+    nw = big.size // mv_w
+    Ws = [big[i * mv_w:(i + 1) * mv_w].view(np.uint32).reshape(4096, 512) for i in range(nw)]
+    mv = (lambda W: R.matvec4(W, s0, b0, x)) if R is not None else (lambda W: O.matvec(4, W, s0, b0, x))
+    n, dt = timed(lambda i: mv(Ws[i % nw]))
+    mv_bytes = 4096 * 512 * 4 + 2 * 4096 * 64 * 2
+    res["config0_matvec"] = {"us": round(dt / n * 1e6, 1), "gbs": round(mv_bytes * n / dt / 1e9, 3),
+                             "sample": f"{n} matvecs over {nw} distinct 8 MB matrices"}
+    del big, Ws
+    # config 1: one expert x router weight
+    n, dt = timed(lambda i: expert(blobs4[(i * 7) % NB], 4, x))
+    res["config1_expert"] = {"us": round(dt / n * 1e6, 1), "gbs": round(size4 * n / dt / 1e9, 3),
+                             "sample": f"{n} expert forwards over {NB} blobs"}
+    # config 2: decode step, 10 routed + shared, weighted sum (cpu_vec_madd)
+    w10 = np.full(K, 0.1, np.float32)
+
+    def step(i, xin=x):
         acc = np.zeros(H, np.float32)
-        for k, b in enumerate(sample_blobs):
-            e = expert(b)
-            acc = R.vec_madd(acc, e, 0.1) if R is not None else acc + 0.1 * e
-        steps += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    step_bytes = len(sample_blobs) * size
-    return {"value": step_bytes * steps / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{steps} config-2 decode steps ({len(sample_blobs)} 4-bit experts each, "
-                      f"{dt:.1f}s, scalar single-thread, gcc -O2)"}
+        for k in range(K):
+            acc = madd(acc, expert(blobs4[(i * 11 + k) % NB], 4, xin), w10[k])
+        return madd(acc, expert(blobs4[(i * 11 + K) % NB], 4, xin), 0.5)
+
+    n, dt = timed(step)
+    res["config2_decode"] = {"us_per_step": round(dt / n * 1e6, 1), "gbs": round((K + 1) * size4 * n / dt / 1e9, 3),
+                             "sample": f"{n} decode steps (11 4-bit experts each) over {NB} blobs"}
+    # config 3: prefill as the reference runs routed experts -- per token
+    # (batched_prefill.h:241-308): tokens/s of the same per-token work
+    X = synth.hidden_vec(synth.rng_for(6), H, (16, H))
+    n, dt = timed(lambda i: step(i, X[i % 16]))
+    res["config3_prefill"] = {"tokens_per_s": round(n / dt, 2), "ms_per_token": round(dt / n * 1e3, 2),
+                              "sample": f"{n} tokens x 11 expert forwards (per-token, as batched_prefill.h "
+                                        f"runs routed experts)"}
+    # config 4: tiered decode b=1 (about a quarter of the routed experts 4-bit)
+    def tstep(i):
+        acc = np.zeros(H, np.float32)
+        for k in range(K):
+            j = i * 11 + k
+            e = expert(blobs4[j % NB], 4, x) if j % 4 == 0 else expert(blobs2[j % 48], 2, x)
+            acc = madd(acc, e, w10[k])
+        return madd(acc, expert(blobs4[(i * 11 + K) % NB], 4, x), 0.5)
+
+    n, dt = timed(tstep)
+    nbytes = sum(size4 if (i * 11 + k) % 4 == 0 else size2 for i in range(1) for k in range(K)) + size4
+    res["config4_tiered_b1"] = {"us_per_step": round(dt / n * 1e6, 1), "gbs": round(nbytes * n / dt / 1e9, 3),
+                                "sample": f"{n} tiered decode steps (2-bit experts: C port)"}
+    c2 = res["config2_decode"]
+    return {"value": c2["gbs"], "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": c2["sample"] + f"; {per:.1f} s per config, blobs generated in {gen_s:.1f} s",
+            "host": host_info(), "configs": res}
 
 
 def main():
@@ -486,7 +563,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (5 configs)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--prefill-warmup", type=int, default=2)
@@ -531,7 +608,7 @@ def main():
     if staging:
         log(f"staging: layer load {staging['layer_load_gbs']} GB/s; per token {staging['stage_us_per_token']} us "
             f"= {staging['stage_gbs']} GB/s; pipelined {staging['stage_pipelined_gbs']} GB/s")
-    cpu = None if args.no_cpu else cpu_baseline(sample, args.cpu_budget)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
     line = {
         "metric": "4-bit expert FFN decode GB/s (% of HBM peak); prefill MoE-layer tokens/s",
         "value": round(dec["value"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
