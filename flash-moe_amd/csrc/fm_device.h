@@ -125,6 +125,57 @@ FM_DEV void fm_load_xgroup(const float *__restrict__ xg, FmXGroup &g) {
     g.sum = s;
 }
 
+// fm_load_xgroup for all G groups of x by a whole workgroup: four adjacent
+// threads per group, 16 elements each (loop over 4 G thread slots; G a
+// multiple of 16 keeps every wave's lanes in step for the shuffles, other G
+// leave whole 4-thread groups idle together).  Same values as fm_load_xgroup.
+template <int BITS>
+FM_DEV void fm_stage_xgroups(const float *__restrict__ x, uint32_t G, FmXGroup *xs) {
+    for (uint32_t i = threadIdx.x; i < ((4 * G + 63) & ~63u); i += blockDim.x) {
+        const uint32_t g = i >> 2, qq = i & 3;
+        const bool live = g < G;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const fm_f4 t = live ? *(const fm_f4 *)(x + 64 * g + 16 * qq + 4 * j) : (fm_f4){0.f, 0.f, 0.f, 0.f};
+            v[4 * j] = t.x;
+            v[4 * j + 1] = t.y;
+            v[4 * j + 2] = t.z;
+            v[4 * j + 3] = t.w;
+        }
+        float mx = 0.f, sm = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if (!live) continue;
+        const int e = fm_group_shift(mx);
+        const float f = fm_exp2i(e);
+        FmXGroup &o = xs[g];
+        if constexpr (BITS == 4) {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float m = (j & 1) ? 0.0625f * f : f;
+                    o.q[4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+                }
+        } else {
+            const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+            for (int n = 0; n < 8; n++) o.q[8 * qq + n] = fm_pack_h2(v[n] * (mt[n] * f), v[8 + n] * (mt[n] * f));
+        }
+        if (qq == 0) {
+            o.sum = sm;
+            o.inv = fm_exp2i(24 - e);
+        }
+    }
+}
+
 // sum over one 4-bit word of code_i * x_i * 2^-24 (8 codes, 9 VALU ops).
 FM_DEV float fm_dot_word4(uint32_t w, const fm_h2 *q, float acc) {
     uint32_t t = w >> 8;

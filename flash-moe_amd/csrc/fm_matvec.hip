@@ -15,7 +15,7 @@
 #include "fm_internal.h"
 
 #define FM_MV_MAX_SPECS 16
-#define FM_MV_NP 4  // row passes per wave
+#define FM_MV_NP 2  // row passes per wave (512 workgroups for 4096 rows: two per CU)
 
 struct FmMvSpec {
     const uint32_t *W;
@@ -62,7 +62,7 @@ __device__ __forceinline__ void fm_mv_body(const FmMvSpec &sp, const float *__re
         }
     }
     // x once per workgroup, as the lane operand layout of every group, in LDS
-    for (uint32_t g = threadIdx.x; g < G; g += blockDim.x) fm_load_xgroup<BITS>(x + 64 * g, xs[g]);
+    fm_stage_xgroups<BITS>(x, G, xs);
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < FM_MV_NP; p++) {
