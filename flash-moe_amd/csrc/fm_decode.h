@@ -50,6 +50,7 @@ struct FmDecodeArgs {
     float norm_eps;
     float *normed;           // fp32 [hidden]
     uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
+    uint64_t *p2;            // few-slot kernel: [S][64 tiles][4 quarters][16 rows][gate, up] tagged partials
 };
 
 // Slot k of token tok (routed slots of token tok read idx/wdev row tok).
@@ -134,6 +135,14 @@ __device__ __forceinline__ void fm_epoch_finish(const FmDecodeArgs &a, uint32_t 
         __hip_atomic_store(a.ws_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (ep == 0xFFFFFFFFu) atomicOr(a.err, FM_STATUS_EPOCH_WRAP);
     }
+}
+
+// Publishes the epoch for the next call from one unit that has, through its
+// own waits, observed a tagged word of every tag user of this call (so each
+// of them has already read the epoch).
+__device__ __forceinline__ void fm_epoch_publish(const FmDecodeArgs &a, uint32_t ep) {
+    __hip_atomic_store(a.ws_epoch, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ep == 0xFFFFFFFFu) atomicOr(a.err, FM_STATUS_EPOCH_WRAP);
 }
 
 // Alternative launchers tried by fm_decode_launch before the eager kernel;

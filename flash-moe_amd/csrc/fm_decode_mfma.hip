@@ -1069,10 +1069,259 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         const int e = a.idx[tid];
         if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
     }
-    // the ends of the hand-off chains: combining items (mode 0) or every down
-    // item (mode 1) count towards publishing the next epoch
-    if (gt == 0 && has && (a.mode == 0 ? last : true))
-        fm_epoch_finish(a, ep, (a.mode == 0 ? 1u : (uint32_t)a.S) * TILES);
+    // Publishing the next epoch.  With the last slot valid, the combining
+    // item of tile 0 has, through its waits, observed every tag user: each
+    // wave of a valid slot read the epoch before its first weight load
+    // returned (loads return in order), which precedes its item's activation
+    // publish, and the combine waited on the outputs of every valid slot,
+    // each computed after all of that slot's activations arrived.  Otherwise
+    // (an invalid last slot: combine waves that poll without having loaded
+    // weights, or mode 1 with no combine) the ends of the hand-off chains
+    // count to the last one.
+    if (gt == 0 && has) {
+        if (a.mode != 0)
+            fm_epoch_finish(a, ep, (uint32_t)a.S * TILES);
+        else if (last && ((T.cvalid >> (a.S - 1)) & 1u)) {
+            if (tile == 0) fm_epoch_publish(a, ep);
+        } else if (last)
+            fm_epoch_finish(a, ep, TILES);
+    }
+}
+
+// ------------------------------------------------- few slots (S <= 4) ----
+// A step of up to four slots (one routed expert, or a few) leaves most CUs
+// idle in the kernels above (64 work items per slot).  Here each of 256
+// workgroups (4 waves, one per slot) takes:
+//   A  slot w, 16 gate/up rows of tile g / 4, the 1024-input quarter g % 4:
+//      partial sums published as tagged words; the quarter-0 workgroup of the
+//      tile adds the four quarters (same order as the kernels above), applies
+//      SwiGLU and publishes the tile's 16 activations;
+//   B  slot w, down rows 16 g .. 16 g + 15 over all 1024 activations;
+//   C  the combine of rows 16 g .. + 15 over the slots -- all of them live in
+//      this workgroup, so it is local (no output hand-off).
+#define FMS_MAXS 4
+#define FMS_GRID 256
+
+struct __attribute__((aligned(16))) FmsLds {
+    fm_h2 xq[2][16][32];          // x of this workgroup's quarter as operand rows
+    float xsum[16], xinv[16];
+    fm_h2 zero[32];
+    fm_h2 aq[FMS_MAXS][2][FMM_GI][32];  // each slot's activations as operand rows
+    float asum[FMS_MAXS][FMM_GI], ainv[FMS_MAXS][FMM_GI];
+    float act[FMS_MAXS][FMM_MAXI];
+    float y[FMS_MAXS][16];
+    uint32_t tr[4][16 * FMM_TS];
+};
+
+__global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a) {
+    __shared__ FmsLds L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave's slot
+    const int n = lane & 15, q = lane >> 4;
+    constexpr uint32_t H = FMM_H, I = FMM_MAXI, GI = FMM_MAXI / 64;
+    const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
+    const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
+    const bool mine = wv < a.S;
+    FM_DX_MARK(0);
+    const uint32_t ep_ld = fm_epoch_load(a);
+    // x of the quarter: 1024 elements, 4 threads per group
+    fm_f4 xr[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 1024 * quarter + 16 * lane + 4 * j);  // every wave: same lines
+    const FmSlot s = fmc_slot(a, mine ? wv : 0);
+    const bool doA = mine && s.valid;
+    const int bits = doA ? s.bits : 4;
+    FmmCodes cg, cu, cdn;
+    fmm_u2 sg, bg, su, bu, sdn, bdn;
+    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * quarter, doA, cg, lane, a.x);
+    fmm_issue_sb(s.gs, s.gb, rowA0, H, 16 * quarter, doA, sg, bg, lane, a.x);
+    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * quarter, doA, cu, lane, a.x);
+    fmm_issue_sb(s.us, s.ub, rowA0, H, 16 * quarter, doA, su, bu, lane, a.x);
+    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
+    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
+    if (tid < 64) {  // wave 0 builds the quarter's 16 operand groups
+        const int gg = tid >> 2, qq = tid & 3;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[4 * j] = xr[j].x;
+            v[4 * j + 1] = xr[j].y;
+            v[4 * j + 2] = xr[j].z;
+            v[4 * j + 3] = xr[j].w;
+        }
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float m = (j & 1) ? 0.0625f * f : f;
+                L.xq[0][gg][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+            }
+        const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+        for (int n2 = 0; n2 < 8; n2++)
+            L.xq[1][gg][8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
+        float sm = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if (qq == 0) {
+            L.xsum[gg] = sm;
+            L.xinv[gg] = fm_exp2i(24 - ex);
+        }
+        if (tid < 32) L.zero[tid] = fm_as_h2(0u);
+    }
+    __syncthreads();
+    FM_DX_MARK(1);
+    const uint32_t ep = fm_epoch_tag(ep_ld);
+    // ---- A: this quarter's partial gate/up sums of the 16 rows ----
+    uint64_t *part = a.p2 + ((size_t)wv * (H / 64) + tile) * 4 * 32;  // [slot][tile][quarter][16 rows][g, u]
+    if (doA) {
+        fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
+        const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][0][0];
+        if (bits == 4) {
+            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+        } else {
+            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+        }
+        FM_DX_MARK(2);
+        float pg = fmm_q_sum(fmm_fold(g0 + g1, sg, bg, &L.xsum[4 * q], &L.xinv[4 * q]));
+        float pu = fmm_q_sum(fmm_fold(u0 + u1, su, bu, &L.xsum[4 * q], &L.xinv[4 * q]));
+        // lanes 0..15: gate of row n, lanes 16..31: up of row n - 16 (the
+        // shuffle runs in the full wave: an inactive source lane reads as 0)
+        const float pu_n = __shfl(pu, (lane - 16) & 63, 64);
+        const float own = lane < 16 ? pg : pu_n;
+        if (quarter != 0 && lane < 32) fm_put_tagged(&part[quarter * 32 + lane], own, ep);
+        if (quarter == 0) {
+            // the tile's activations: the other three quarters' partials, in the order (q0 + q1) + (q2 + q3)
+            uint64_t t[3];
+            const bool rd = lane < 32;
+#pragma unroll
+            for (int j = 0; j < 3; j++) t[j] = rd ? fm_get_tagged(&part[(j + 1) * 32 + lane]) : ((uint64_t)ep << 32);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int j = 0; j < 3; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+                if (__all(ready)) break;
+#pragma unroll
+                for (int j = 0; j < 3; j++)
+                    if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(&part[(j + 1) * 32 + lane]);
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+            const float p1 = __uint_as_float((uint32_t)t[0]), p2 = __uint_as_float((uint32_t)t[1]);
+            const float p3 = __uint_as_float((uint32_t)t[2]);
+            const float tot = (own + p1) + (p2 + p3);
+            const float up = __shfl(tot, (lane & 15) + 16, 64);
+            if (lane < 16) fm_put_tagged(&a.act2[(size_t)wv * I + rowA0 + lane], fm_silu_mul(tot, up), ep);
+        }
+    }
+    FM_DX_MARK(3);
+    // ---- B: the slot's 1024 activations, then 16 down rows ----
+    if (doA) {
+        const uint64_t *src = a.act2 + (size_t)wv * I;
+        uint64_t t[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) t[j] = fm_get_tagged(src + 64 * j + lane);
+        uint32_t it = 0;
+        do {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < 16; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+            if (__all(ready)) break;
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(src + 64 * j + lane);
+        } while (++it < FM_SPIN_MAX);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+        FM_DX_MARK(4);
+#pragma unroll
+        for (int j = 0; j < 16; j++) L.act[wv][64 * j + lane] = __uint_as_float((uint32_t)t[j]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        // per group (4 lanes x 16 elements): sum, scale 2^e, operand rows
+        const int lay = bits == 4 ? 0 : 1;
+        const uint32_t gg = lane >> 2, qq = lane & 3;
+        const float *ag = &L.act[wv][64 * gg + 16 * qq];
+        float sm = 0.f, mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            sm += ag[j];
+            mx = fmaxf(mx, fabsf(ag[j]));
+        }
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
+        if (qq == 0) {
+            L.asum[wv][gg] = sm;
+            L.ainv[wv][gg] = fm_exp2i(24 - ex);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) fmm_build_pair(&L.act[wv][64 * gg], bits, 8 * qq + e, f, &L.aq[wv][lay][gg][0]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        FM_DX_MARK(5);
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        if (bits == 4)
+            fmm_mma<4>(cdn, &L.aq[wv][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
+        else
+            fmm_mma<2>(cdn, &L.aq[wv][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
+        const float y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[wv][4 * q], &L.ainv[wv][4 * q]));
+        if (lane < 16) {
+            if (a.mode == 1)
+                a.expert_out[(size_t)wv * H + rowB0 + n] = y;
+            else
+                L.y[wv][n] = y;
+        }
+    }
+    FM_DX_MARK(6);
+    __syncthreads();
+    // Every wave of a valid slot waited above for the activations of all 64
+    // tiles, each published after the tile's four quarters tagged their
+    // partials: so every tag user of this call has read the epoch, and one
+    // plain store publishes it for the next call (no completion counter).
+    if (g == 0 && tid == 0) fm_epoch_publish(a, ep);
+    // ---- C: rows 16 g .. + 15 over the slots, in cpu_vec_madd order ----
+    if (a.mode == 0 && wv == 0 && lane < 16) {
+        const uint32_t row = rowB0 + lane;
+        float moe = 0.f;
+#pragma unroll
+        for (int k = 0; k < FMS_MAXS; k++) {
+            if (k < a.K) {
+                const FmSlot sk = fmc_slot(a, k);
+                if (sk.valid) moe = __fadd_rn(moe, __fmul_rn(sk.weight, L.y[k][lane]));
+            }
+        }
+        float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+        const float sw = (a.has_shared || a.shared_y)
+                             ? (a.shared_score ? fm_sigmoid(a.shared_score[0]) : a.shared_w_host)
+                             : 0.f;
+        if (a.has_shared) {
+            const FmSlot ss = fmc_slot(a, a.S - 1);
+            o = __fadd_rn(o, __fmul_rn(sw, ss.valid ? L.y[a.S - 1][lane] : 0.f));
+        } else if (a.shared_y) {
+            o = __fadd_rn(o, __fmul_rn(sw, a.shared_y[row]));
+        }
+        a.out[row] = o;
+        if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+    }
+    if (a.pool_mode && g == 0 && tid < a.K) {
+        const int e = a.idx[tid];
+        if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+    }
+    FM_DX_MARK(7);
 }
 
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
@@ -1091,6 +1340,14 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
+    // up to four slots of one token (no fused norm): the split kernel
+    if (a.ntok <= 1 && a.S <= FMS_MAXS && !a.norm_w) {
+        const char *no_split = getenv("FMOE_DECODE_NO_SPLIT");
+        if (!(no_split && *no_split)) {
+            hipLaunchKernelGGL(fm_decode_split_kernel, dim3(FMS_GRID), dim3(256), 0, st, a);
+            return fm_check_launch("fm_decode_split_kernel");
+        }
+    }
     static int per_cu_c = -1;
     if (per_cu_c < 0 &&
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel, FMC_THREADS, 0) != hipSuccess)
