@@ -195,7 +195,7 @@ def bench_decode(args, dev):
         "value": step_bytes / (step_ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": pmc_traffic("decode_config2_pmc.json"),
-                     "kernel": "fm_decode_mfma_kernel (one fm_moe_decode_pool call)",
+                     "kernel": "fm_decode_cu_kernel (one fm_moe_decode_pool call)",
                      "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes,
                      "kernel_us_with_fused_rms_norm": norm_ms * 1e3},
         "layer_step": {"path": "fm_moe_forward: router + shared-gate matvecs (4-bit) -> routing -> fused experts",
