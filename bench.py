@@ -205,6 +205,55 @@ def bench_decode(args, dev):
     return res, sample_blobs
 
 
+def bench_qwen35(args, dev):
+    """The reference's other model shape (Qwen3.5-35B-A3B: hidden 2048,
+    moe_intermediate 512, 256 experts, K = 8 + a shared expert of 512):
+    decode step (routing + fused experts) as a HIP graph, and the kernel alone."""
+    import numpy as np
+    import torch
+    import fmoe_amd as fm
+    from fmoe_amd import synth
+    h, i_, e_, k_ = 2048, 512, 256, 8
+    blobs = [synth.expert_blob((3500, e), h, i_, 4) for e in range(e_)]
+    pool = fm.DevicePool(blobs, [4] * e_, h, i_)
+    del blobs
+    sh_dev = [torch.from_numpy(synth.expert_blob((3501, j), h, i_, 4)).to(dev) for j in range(16)]
+    shared = [fm.experts_from_blob(d, 4, h, i_) for d in sh_dev]
+    rng = synth.rng_for(3502)
+    nsteps = args.warmup + args.steps
+    logits = torch.from_numpy(rng.normal(0, 1, (nsteps, e_)).astype(np.float32)).to(dev)
+    scores = torch.from_numpy(rng.normal(0, 1, nsteps).astype(np.float32)).to(dev)
+    x = torch.from_numpy(synth.hidden_vec(rng, h)).to(dev)
+    hm = torch.from_numpy(rng.normal(0, 1, h).astype(np.float32)).to(dev)
+    idx = torch.empty((nsteps, k_), dtype=torch.int32, device=dev)
+    w = torch.empty((nsteps, k_), dtype=torch.float32, device=dev)
+    ws = fm.workspace(fm.decode_workspace_bytes(k_ + 1, h, i_), dev)
+    out = torch.empty(h, dtype=torch.float32, device=dev)
+
+    def dec(j):
+        fm.moe_decode_pool(pool, idx[j], w[j], x, out, ws, shared=shared[j % 16], shared_bits=4,
+                           shared_score=scores[j:j + 1], h_mid=hm)
+
+    def step(j):
+        fm.route_topk(logits[j:j + 1], k_, idx[j], w[j])
+        dec(j)
+
+    for j in range(args.warmup):
+        step(j)
+    g = graph_of(step, range(args.warmup, nsteps))
+    step_ms = time_graph(g, args.steps)
+    del g
+    g = graph_of(dec, range(args.warmup, nsteps))
+    kern_ms = time_graph(g, args.steps)
+    del g
+    if fm.workspace_status(ws):
+        raise SystemExit("qwen3.5-35b decode: workspace status set")
+    nbytes = (k_ + 1) * fm.layout_of(h, i_, 64, 4).size + h * 4 * 3
+    return {"workload": "Qwen3.5-35B-A3B shape: hidden 2048, inter 512, 256 experts, top-8 + shared, 4-bit",
+            "step_us": round(step_ms * 1e3, 2), "kernel_us": round(kern_ms * 1e3, 2), "bytes": nbytes,
+            "kernel_gbs": round(nbytes / kern_ms / 1e6, 1), "kernel_hbm_frac": round(nbytes / kern_ms / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 def bench_prefill(args, dev, pool):
     """Config 3: 512 tokens, 512 experts, top-10 over Zipf(1.1) logits + shared
     expert, one MoE layer = routing + grouped expert GEMMs + combine."""
@@ -596,6 +645,8 @@ def main():
     small = bench_small(args, dev, args._pool)
     log(f"config 0 matvec: {small['config0_matvec']['us']} us = {small['config0_matvec']['gbs']} GB/s; "
         f"config 1 expert: {small['config1_expert']['us']} us = {small['config1_expert']['gbs']} GB/s")
+    q35 = bench_qwen35(args, dev)
+    log(f"qwen3.5-35b shape: step {q35['step_us']} us, kernel {q35['kernel_us']} us = {q35['kernel_gbs']} GB/s")
     pre = None if args.no_prefill else bench_prefill(args, dev, args._pool)
     if pre:
         log(f"prefill: {pre['ms']:.3f} ms/layer, {pre['tokens_per_s']:.0f} tok/s, {pre['hbm_gbs']:.0f} GB/s, "
@@ -624,6 +675,7 @@ def main():
         "roofline": dec["roofline"],
         "layer_step": dec["layer_step"],
         "single": small,
+        "qwen35_shape": q35,
         "prefill": None if pre is None else {
             "workload": "config 3: 512 tokens, 512 experts, top-10 Zipf(1.1) + shared, grouped MFMA dequant-GEMM",
             "tokens_per_s": round(pre["tokens_per_s"]), "ms_per_layer": pre["ms"],
