@@ -167,6 +167,9 @@ struct FmmCodes {
 // `dummy` instead, so the number of loads in flight never depends on a branch
 // (the compiler's wait counts stay exact instead of falling back to "wait for
 // everything").  bits must be 2 or 4 either way.
+// NG (16 or 8): groups of the unit.  With 8 groups a 4-bit row run is one
+// piece (4 loads) and a 2-bit one half a piece (lanes n >= 8 repeat lane n - 8).
+template <int NG = 16>
 FM_DEV void fmm_issue_codes(const uint32_t *W, int bits, uint32_t row0, uint32_t in_dim, uint32_t g0, bool ok,
                             FmmCodes &cd, int lane, const void *dummy) {
     const int n = lane & 15, kq = lane >> 4;
@@ -175,27 +178,33 @@ FM_DEV void fmm_issue_codes(const uint32_t *W, int bits, uint32_t row0, uint32_t
         W = (const uint32_t *)dummy;
         row0 = g0 = 0;
     }
-    // always 8 loads: a 2-bit row piece is 4 of them, its other 4 repeat the
-    // same addresses (cache hits) so the load count never depends on bits
+    // always 8 loads (4 with 8 groups): a 2-bit row piece is 4 of them, its
+    // other 4 repeat the same addresses (cache hits) so the load count never
+    // depends on bits
+    const int nw = (NG == 8 && bits == 2) ? (n & 7) : n;
 #pragma unroll
-    for (int p = 0; p < 2; p++) {
+    for (int p = 0; p < NG / 8; p++) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t row = row0 + 4 * j + kq;
             const uint32_t po = (ok && bits == 4) ? g0 * wpg + 64 * p : (ok ? g0 * wpg : 0);
-            cd.c[4 * p + j] = fm_ldg_u4_nt(W + (size_t)row * wpr + po + 4 * n);
+            cd.c[4 * p + j] = fm_ldg_u4_nt(W + (size_t)row * wpr + po + 4 * nw);
         }
     }
 }
 
 // The scale / bias runs of fmm_issue (lane (n, kq): row row0 + n, groups
 // g0 + 4 kq .. + 3), branch-free like fmm_issue_codes.
+// With NG = 8 the lanes kq >= 2 hold no group of the unit: zero.
+template <int NG = 16>
 FM_DEV void fmm_issue_sb(const uint16_t *S, const uint16_t *B, uint32_t row0, uint32_t in_dim, uint32_t g0, bool ok,
                          fmm_u2 &sc, fmm_u2 &bi, int lane, const void *dummy) {
     const int n = lane & 15, kq = lane >> 4;
-    const size_t o = ok ? (size_t)(row0 + n) * (in_dim / 64) + g0 + 4 * kq : 0;
-    sc = *(const FM_GLOBAL fmm_u2 *)(ok ? S + o : (const uint16_t *)dummy);
-    bi = *(const FM_GLOBAL fmm_u2 *)(ok ? B + o : (const uint16_t *)dummy);
+    const bool mine = ok && 4 * kq < NG;
+    const size_t o = mine ? (size_t)(row0 + n) * (in_dim / 64) + g0 + 4 * kq : 0;
+    sc = *(const FM_GLOBAL fmm_u2 *)(mine ? S + o : (const uint16_t *)dummy);
+    bi = *(const FM_GLOBAL fmm_u2 *)(mine ? B + o : (const uint16_t *)dummy);
+    if (NG == 8 && !mine) sc = bi = (fmm_u2){0u, 0u};
 }
 
 // Issue the loads of 16 rows x 16 groups (groups g0 .. g0+15) of one matrix.
@@ -234,7 +243,7 @@ FM_DEV uint32_t fmm_comp(const fm_u4 &v, int j) { return j == 0 ? v.x : j == 1 ?
 // The x operand row m carries group g0 + m and is non-zero only in the slot
 // that holds that group.  The LDS x operand of step j+1 is read during step
 // j; scheduling barriers keep the compiler from hoisting further reads.
-template <int BITS>
+template <int BITS, int NG = 16>  // NG = 8: groups 0..7 only (16 MFMAs)
 FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, uint32_t *T, fmm_f4 &d0,
                     fmm_f4 &d1, int lane) {
     const int m = lane & 15, kq = lane >> 4;
@@ -258,7 +267,7 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
         const fmm_h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
         const bool kq_on = (kq >> 1) == (m & 1);
 #pragma unroll
-        for (int p = 0; p < 2; p++) {
+        for (int p = 0; p < NG / 8; p++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) *(fm_u4 *)&T[(4 * j + kq) * FMM_TS + 4 * m] = cd.c[4 * p + j];
             fm_u4 v[4];
@@ -289,7 +298,7 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
         fm_u4 v[4];
 #pragma unroll
         for (int h = 0; h < 4; h++) v[h] = *(const fm_u4 *)&T[m * FMM_TS + 16 * h + 4 * kq];
-        constexpr int NJ = 32 / NP;
+        constexpr int NJ = 2 * NG / NP;
 #pragma unroll
         for (int jj = 0; jj < NJ; jj++) {
             const int j = p * NJ + jj;
@@ -777,6 +786,10 @@ FM_DEV void fmc_item_sync(uint32_t *ctr, uint32_t &target) {
     asm volatile("" ::: "memory");
 }
 
+// NG = input groups of one wave's share of a row (16: hidden 4096 / inter 1024;
+// 8: hidden 2048 / inter 512).  hidden = 256 NG, inter = hidden / 4, so the
+// gate/up tiles (16 rows) and the down tiles (64 rows) of a slot pair up.
+template <int NG>
 __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeArgs a) {
     __shared__ FmcLds L;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -784,7 +797,8 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     const int wv = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
     const int gt = tid & 255;  // thread within the item
     const int n = lane & 15, q = lane >> 4;
-    constexpr uint32_t H = FMM_H, I = FMM_MAXI, GI = FMM_MAXI / 64, TILES = FMM_H / 64;  // == I / 16
+    constexpr uint32_t H = 256 * NG, I = 64 * NG, GI = NG, GH = 4 * NG, TILES = 4 * NG;  // TILES == I / 16
+    static_assert(H <= FMM_H && I <= FMM_MAXI, "LDS is sized for hidden 4096 / inter 1024");
     const uint32_t item = blockIdx.x + gridDim.x * (uint32_t)grp;
     const bool has = item < (uint32_t)a.S * TILES;
     const int k = has ? (int)(item / TILES) : 0;  // the item's slot
@@ -801,7 +815,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // cache); item 0 turns them into operand rows below
     fm_f4 xr[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * gt + 4 * j);
+    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (gt < (int)GH * 4 ? gt : 0) + 4 * j);
     const FmSlot s = fmc_slot(a, k);
     const bool doA = has && s.valid;
     // Every gate/up load of the item.  Loads issue in order and block while
@@ -812,8 +826,8 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     FmmCodes cg, cu, cdn;
     fmm_u2 sdn = {0, 0}, bdn = {0, 0}, scl[4] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
     const int bits = doA ? s.bits : 4;
-    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * wv, doA, cg, lane, a.x);
-    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * wv, doA, cu, lane, a.x);
+    fmm_issue_codes<NG>(s.gw, bits, rowA0, H, NG * wv, doA, cg, lane, a.x);
+    fmm_issue_codes<NG>(s.uw, bits, rowA0, H, NG * wv, doA, cu, lane, a.x);
     // the tile's gate/up scales and biases: 16 rows x 64 groups = 2 KB per
     // array, contiguous; wave wv loads rows 4 wv .. 4 wv + 3 of each (full
     // lines) and the item shares them through LDS
@@ -821,8 +835,8 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         const uint16_t *arr[4] = {s.gs, s.gb, s.us, s.ub};
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            scl[j] = *(const FM_GLOBAL fmm_u2 *)(doA ? arr[j] + (size_t)(rowA0 + 4 * wv) * FMM_GH + 4 * lane
-                                                       : (const uint16_t *)a.x);
+            scl[j] = *(const FM_GLOBAL fmm_u2 *)((doA && lane < (int)GH) ? arr[j] + (size_t)(rowA0 + 4 * wv) * GH + 4 * lane
+                                                                         : (const uint16_t *)a.x);
     }
     FM_DX_MARK(1);
     const bool last = has && a.mode == 0 && k == a.S - 1;
@@ -845,6 +859,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     if (grp == 0) {
         if (tid < 32) L.zero[tid] = fm_as_h2(0u);
         const int g = tid >> 2, qq = tid & 3;
+        const bool gok = g < (int)GH;
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -865,18 +880,18 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float m = (j & 1) ? 0.0625f * f : f;
-                L.xq[0][g][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+                if (gok) L.xq[0][g][4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
             }
         const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
 #pragma unroll
         for (int n2 = 0; n2 < 8; n2++)
-            L.xq[1][g][8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
+            if (gok) L.xq[1][g][8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
         float sm = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
         sm += __shfl_xor(sm, 1, 64);
         sm += __shfl_xor(sm, 2, 64);
-        if (qq == 0) {
+        if (qq == 0 && gok) {
             L.xsum[g] = sm;
             L.xinv[g] = fm_exp2i(24 - ex);
         }
@@ -899,24 +914,29 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // ---- A: gate/up partials of 16 rows over this wave's 16 groups ----
     if (doA) {
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
-        const fm_h2 *xq = &L.xq[s.bits == 4 ? 0 : 1][16 * wv][0];
+        const fm_h2 *xq = &L.xq[s.bits == 4 ? 0 : 1][NG * wv][0];
         if (s.bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
-            fmm_mma<4>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
+            fmm_mma<4, NG>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
+            fmm_mma<4, NG>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
         } else {
-            fmm_mma<2>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
-            fmm_mma<2>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
+            fmm_mma<2, NG>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
+            fmm_mma<2, NG>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
         }
+        // scale runs: GH / 4 lanes per row (4 groups = 2 words each)
+        if (lane < (int)GH) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) *(fmm_u2 *)&T.scl[j][4 * wv + (lane >> 4)][2 * (lane & 15)] = scl[j];
+            for (int j = 0; j < 4; j++)
+                *(fmm_u2 *)&T.scl[j][4 * wv + lane / (GH / 4)][2 * (lane % (GH / 4))] = scl[j];
+        }
         fmc_item_sync(&T.sync, phase);
-        // lane (row n, q) folds groups 16 wv + 4 q .. + 3 of row n
-        const int c0 = 8 * wv + 2 * q;
+        // lane (row n, q) folds groups NG wv + 4 q .. + 3 of row n (NG = 8: q < 2 only)
+        const bool qok = 4 * q < NG;
+        const int c0 = (NG / 2) * wv + 2 * (qok ? q : 0);
         const fmm_u2 sg = *(const fmm_u2 *)&T.scl[0][n][c0], bg = *(const fmm_u2 *)&T.scl[1][n][c0];
         const fmm_u2 su = *(const fmm_u2 *)&T.scl[2][n][c0], bu = *(const fmm_u2 *)&T.scl[3][n][c0];
-        const float *gs4 = &L.xsum[16 * wv + 4 * q], *gi4 = &L.xinv[16 * wv + 4 * q];
-        float pg = fmm_fold(g0 + g1, sg, bg, gs4, gi4);
-        float pu = fmm_fold(u0 + u1, su, bu, gs4, gi4);
+        const float *gs4 = &L.xsum[NG * wv + 4 * (qok ? q : 0)], *gi4 = &L.xinv[NG * wv + 4 * (qok ? q : 0)];
+        float pg = qok ? fmm_fold(g0 + g1, sg, bg, gs4, gi4) : 0.f;
+        float pu = qok ? fmm_fold(u0 + u1, su, bu, gs4, gi4) : 0.f;
         pg = fmm_q_sum(pg);
         pu = fmm_q_sum(pu);
         if (lane < 16) {
@@ -932,13 +952,13 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         fm_put_tagged(&a.act2[(size_t)k * I + rowA0 + gt], fm_silu_mul(g, u), ep);
     }
     // the down rows (queue behind every gate/up request of the CU)
-    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
-    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
+    fmm_issue_codes<NG>(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
+    fmm_issue_sb<NG>(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
     FM_DX_MARK(4);
 
     // ---- B: the slot's activations (every A tile of the slot), then 16 down rows per wave ----
     if (doA) {
-        constexpr int MAXQ = FMM_MAXI / 256;
+        constexpr int MAXQ = I / 256;
         uint64_t t[MAXQ];
         const uint64_t *src = a.act2 + (size_t)k * I;
 #pragma unroll
@@ -958,7 +978,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         for (int j = 0; j < MAXQ; j++) T.act[j * 256 + gt] = __uint_as_float((uint32_t)t[j]);
     }
     fmc_item_sync(&T.sync, phase);
-    if (doA) {
+    if (doA && gt < 16 * (int)GI) {
         // per group (16 threads x 4 elements): sum, operand scale 2^e, operand rows
         const int lay = s.bits == 4 ? 0 : 1;
         const uint32_t g = gt >> 4;
@@ -982,10 +1002,11 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &T.aq[s.bits == 4 ? 0 : 1][0][0];
         if (s.bits == 4)
-            fmm_mma<4>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+            fmm_mma<4, NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
         else
-            fmm_mma<2>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
-        float y = fmm_fold(d0 + d1, sdn, bdn, &T.asum[4 * q], &T.ainv[4 * q]);
+            fmm_mma<2, NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+        const bool qok = 4 * q < NG;
+        float y = qok ? fmm_fold(d0 + d1, sdn, bdn, &T.asum[4 * (qok ? q : 0)], &T.ainv[4 * (qok ? q : 0)]) : 0.f;
         y = fmm_q_sum(y);
         const uint32_t row = rowB0 + n;
         if (lane < 16) {
@@ -1326,6 +1347,23 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
 
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
+    const int cus = fm_num_cus();
+    // hidden 2048 / inter 512 (the Qwen3.5-35B-A3B expert shape): the
+    // one-workgroup-per-CU kernel with 8-group units, one token whose items
+    // fit three per CU
+    if (a.hidden == 2048 && a.inter == 512) {
+        static int per_cu_8 = -1;
+        if (per_cu_8 < 0 &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_8, fm_decode_cu_kernel<8>, FMC_THREADS, 0) !=
+                hipSuccess)
+            per_cu_8 = 0;
+        if (a.ntok <= 1 && a.spt == a.S && per_cu_8 >= 1 && (uint32_t)a.S * 32 <= (uint32_t)(FMC_NG * cus) &&
+            a.S <= FM_MAX_SLOTS) {
+            hipLaunchKernelGGL(fm_decode_cu_kernel<8>, dim3(cus), dim3(FMC_THREADS), 0, st, a);
+            return fm_check_launch("fm_decode_cu_kernel");
+        }
+        return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: 2048/512 takes one token");
+    }
     if (a.hidden != FMM_H || a.inter != FMM_MAXI)
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: shape");
     static int per_cu = -1, per_cu_mp = -1;
@@ -1350,16 +1388,15 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     }
     static int per_cu_c = -1;
     if (per_cu_c < 0 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel, FMC_THREADS, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel<16>, FMC_THREADS, 0) != hipSuccess)
         per_cu_c = 0;
-    const int cus = fm_num_cus();
     // one token whose items fit three per CU: the one-workgroup-per-CU kernel
     // (FMOE_DECODE_NO_CU set in the environment: the three-workgroup kernel,
     // which tests compare it with)
     const char *no_cu = getenv("FMOE_DECODE_NO_CU");
     if (a.ntok <= 1 && per_cu_c >= 1 && (uint32_t)a.S * (FMM_H / 64) <= (uint32_t)(FMC_NG * cus) &&
         a.S <= FM_MAX_SLOTS && !(no_cu && *no_cu)) {
-        hipLaunchKernelGGL(fm_decode_cu_kernel, dim3(cus), dim3(FMC_THREADS), 0, st, a);
+        hipLaunchKernelGGL(fm_decode_cu_kernel<16>, dim3(cus), dim3(FMC_THREADS), 0, st, a);
         return fm_check_launch("fm_decode_cu_kernel");
     }
     const uint32_t tiles = a.inter / 16 > a.hidden / 64 ? a.inter / 16 : a.hidden / 64;

@@ -99,7 +99,9 @@ def _decode_inputs(seed, K, bits_list, hidden=HIDDEN, inter=INTER):
 
 @pytest.mark.parametrize("K,bitmode,hidden,inter", [(10, "4", HIDDEN, INTER), (10, "tiered", HIDDEN, INTER),
                                                      (1, "4", HIDDEN, INTER), (16, "2", HIDDEN, INTER),
-                                                     (4, "4", 2048, 512), (3, "tiered", 1024, 2048)])
+                                                     (4, "4", 2048, 512), (3, "tiered", 1024, 2048),
+                                                     (8, "tiered", 2048, 512), (16, "2", 2048, 512),
+                                                     (1, "4", 2048, 512)])
 def test_moe_decode_host_routed(orc, dev, K, bitmode, hidden, inter):
     import torch
     say("moe_decode", K, bitmode, hidden, inter)
@@ -436,4 +438,46 @@ def test_decode_pool_both_mfma_kernels(orc, dev, pool64, kernel, monkeypatch):
                          shared_blob=shared_blob, shared_bits=2, shared_score=-0.4, h_mid=hm)
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
     assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, nw, 1e-6)) <= TOL_F32
+    assert fm.workspace_status(ws) == 0
+
+
+@pytest.mark.parametrize("K", [8, 16])
+@pytest.mark.parametrize("kernel", ["mfma", "eager"])
+def test_decode_2048_512_kernels(orc, dev, monkeypatch, K, kernel):
+    """The hidden 2048 / inter 512 shape (Qwen3.5-35B-A3B experts): the MFMA
+    one-workgroup-per-CU kernel with 8-group units, and the v_dot2 kernel it
+    replaces (FMOE_DECODE_KERNEL=eager), on a tiered pool with the fused norm,
+    three calls on one workspace, each against the oracle."""
+    import torch
+    say("decode 2048/512", K, kernel)
+    if kernel == "eager":
+        monkeypatch.setenv("FMOE_DECODE_KERNEL", "eager")
+    H2, I2, E = 2048, 512, 48
+    bits = [4 if e % 3 else 2 for e in range(E)]
+    blobs = experts(range(8800, 8800 + E), bits, H2, I2)
+    pool = fm.DevicePool(blobs, bits, H2, I2)
+    shared_blob = synth.expert_blob((8900, K), H2, I2, 4)
+    dsh = T(shared_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, H2, I2)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, H2, I2), dev)
+    out = torch.empty(H2, dtype=torch.float32, device=dev)
+    normed = torch.empty(H2, dtype=torch.float32, device=dev)
+    rng = synth.rng_for(88, K, kernel == "mfma")
+    nw = synth.bf16_bits(rng.normal(1, 0.2, H2).astype(np.float32))
+    for rep in range(3):
+        lg = rng.normal(0, 1, (1, E)).astype(np.float32)
+        x = synth.hidden_vec(rng, H2)
+        hm = rng.normal(0, 1, H2).astype(np.float32)
+        g = np.array([rng.normal()], np.float32)
+        idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+        w = torch.empty((1, K), dtype=torch.float32, device=dev)
+        fm.route_topk(T(lg, dev), K, idx, w)
+        fm.moe_decode_pool_norm(pool, idx, w, T(x, dev), out, ws, T(nw.view(np.int16), dev), 1e-6, normed,
+                                shared=sh, shared_bits=4, shared_score=T(g, dev), h_mid=T(hm, dev))
+        torch.cuda.synchronize()
+        ri, rw = orc.route(lg, K)
+        ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], x, H2, I2,
+                             shared_blob=shared_blob, shared_bits=4, shared_score=float(g[0]), h_mid=hm)
+        assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, rep
+        assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, nw, 1e-6)) <= TOL_F32, rep
     assert fm.workspace_status(ws) == 0

@@ -61,8 +61,9 @@ def test_matvec_range(orc, dev, bits, regime):
 @pytest.mark.parametrize("regime", REGIMES)
 @pytest.mark.parametrize("hidden,inter", [(HIDDEN, INTER), (2048, 512)])
 def test_decode_range(orc, dev, regime, hidden, inter):
-    """Decode step, 4-bit and 2-bit slots mixed (the MFMA kernel at 4096/1024,
-    the v_dot2 kernels at 2048/512); per-expert outputs and the combine."""
+    """Decode step, 4-bit and 2-bit slots mixed (the per-CU MFMA kernel with
+    16-group units at 4096/1024, with 8-group units at 2048/512); per-expert
+    outputs and the combine."""
     import torch
     say("decode range", regime, hidden, inter)
     K = 6
