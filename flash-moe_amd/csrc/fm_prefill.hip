@@ -323,10 +323,10 @@ __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageReg
     if (t < PF_TOK * PF_GPP) st.xsum[(t >> 4) & 7][t & 15] = r.xs;
 }
 
-// Row-tile count of a workgroup: when the whole input fits the two token
-// stages (np <= 2 pieces, e.g. the down projection's 1024 inputs) the chunk's
-// operands stay resident in LDS and one workgroup walks PF_RL row blocks, the
-// weight ring running on across them; otherwise one row block per workgroup.
+// Row-tile count of a workgroup: when the whole input fits the stages the
+// chunk's operands stay resident in LDS and one workgroup walks PF_RL (PF_RL8
+// for the eight-stage kernel) row blocks, the weight ring running on across
+// them; otherwise one row block per workgroup.
 #ifndef PF_WLOAD
 #define PF_WLOAD fm_ldg_u4_nt  // weight pieces: streamed once per chunk
 #endif
@@ -339,10 +339,11 @@ __device__ __forceinline__ void pf_stage_store(PfStage<LO> &st, const PfStageReg
 #ifndef PF_RL8
 #define PF_RL8 4    // row blocks of a workgroup holding eight stages (8 waves: 512 rows of 1024)
 #endif
-// nst: token stages the workgroup holds (2, or 8 for the one-per-CU gate/up kernel)
-__host__ __device__ inline int pf_row_tiles(uint32_t in_dim, int nst) {
-    return in_dim / 64 <= (uint32_t)nst * PF_GPP ? (nst == 8 ? PF_RL8 : PF_RL) : 1;
-}
+__host__ __device__ constexpr int pf_row_tiles(bool res, int nst) { return res ? (nst == 8 ? PF_RL8 : PF_RL) : 1; }
+// weight ring depth (pieces in flight per wave); the resident kernels' step
+// counts (pieces x row tiles) are multiples of it
+__host__ __device__ constexpr int pf_ring(int nst) { return nst == 8 ? PF_RING8 : PF_RING; }
+static_assert(PF_RL % PF_RING == 0 && PF_RL8 % PF_RING8 == 0, "a resident workgroup's steps fill whole ring turns");
 
 // DUAL: the workgroup computes the same rows of two matrices (gate and up)
 // from one token stage, so the chunk's operands stream once for both.
@@ -434,17 +435,92 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
             if (gg & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
         }
     };
-    // Ring of PF_RING pieces with static slots: the step loop is unrolled by
-    // PF_RING, so no register ever moves between slots (a move would wait for
-    // the slot's loads) and every step issues the same loads -- the in-order
-    // wait counts stay exact and PF_RING - 1 pieces stay in flight while one
-    // is computed.
-    constexpr int R = NST == 8 ? PF_RING8 : PF_RING;
-    fm_f4v acc = (fm_f4v){0.f, 0.f, 0.f, 0.f}, acc2 = acc;
+    // DUAL: the gate and up pieces of the same rows together -- each group's
+    // codes of both matrices come out of the transpose buffer first (raw
+    // words), then the group's operands and sums are read from the stage once
+    // for the four MFMAs and two folds
+    auto compute2 = [&](const PfPiece<BITS> &cg, const PfPiece<BITS> &cu, const PfStage<LO> &cs, fm_f4v &acc,
+                        fm_f4v &acc2) {
+        constexpr int HG = BITS == 4 ? PF_GPP / 2 : PF_GPP;  // groups per transpose pass
+        const uint32_t sg[4] = {cg.s.x, cg.s.y, cg.s.z, cg.s.w}, bg[4] = {cg.b.x, cg.b.y, cg.b.z, cg.b.w};
+        const uint32_t su[4] = {cu.s.x, cu.s.y, cu.s.z, cu.s.w}, bu[4] = {cu.b.x, cu.b.y, cu.b.z, cu.b.w};
+#pragma unroll
+        for (int hf = 0; hf < PF_GPP / HG; hf++) {
+            uint64_t rg[HG], ru[HG];  // 4-bit: two words per group; 2-bit: one
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const PfPiece<BITS> &cur = m == 0 ? cg : cu;
+#pragma unroll
+                for (int j = 0; j < NL; j++)
+                    if (BITS != 4 || (lw >> 5) == hf) *(fm_u4 *)&T[(RS * j + lrow) * PF_TS + lw - 32 * hf] = cur.c[j];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k = 0; k < HG; k++) {
+                    uint64_t w;
+                    if constexpr (BITS == 4)
+                        w = *(const uint64_t *)&T[n * PF_TS + 8 * k + 2 * kq];
+                    else
+                        w = T[n * PF_TS + 4 * k + kq];
+                    (m == 0 ? rg : ru)[k] = w;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int k = 0; k < HG; k++) {
+                const int gg = HG * hf + k;
+                fm_h8 g0, g1, u0, u1;
+                if constexpr (BITS == 4) {
+                    g0 = pf_codes<4>((uint32_t)rg[k], 0);
+                    g1 = pf_codes<4>((uint32_t)(rg[k] >> 32), 0);
+                    u0 = pf_codes<4>((uint32_t)ru[k], 0);
+                    u1 = pf_codes<4>((uint32_t)(ru[k] >> 32), 0);
+                } else {
+                    g0 = pf_codes<2>((uint32_t)rg[k], 0);
+                    g1 = pf_codes<2>((uint32_t)rg[k], 1);
+                    u0 = pf_codes<2>((uint32_t)ru[k], 0);
+                    u1 = pf_codes<2>((uint32_t)ru[k], 1);
+                }
+                const float scg = fm_bf16_to_f32((uint16_t)(sg[gg >> 1] >> (16 * (gg & 1))));
+                const float big = fm_bf16_to_f32((uint16_t)(bg[gg >> 1] >> (16 * (gg & 1))));
+                const float scu = fm_bf16_to_f32((uint16_t)(su[gg >> 1] >> (16 * (gg & 1))));
+                const float biu = fm_bf16_to_f32((uint16_t)(bu[gg >> 1] >> (16 * (gg & 1))));
+                const fm_h8 x0 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq]);
+                const fm_h8 x1 = __builtin_bit_cast(fm_h8, *(const fm_u4 *)&cs.xop[0][n][32 * gg + 8 * kq + 4]);
+                fm_f4v dg = {0.f, 0.f, 0.f, 0.f}, du = dg;
+                dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, g0, dg, 0, 0, 0);
+                du = __builtin_amdgcn_mfma_f32_16x16x32_f16(x0, u0, du, 0, 0, 0);
+                dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, g1, dg, 0, 0, 0);
+                du = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, u1, du, 0, 0, 0);
+                const fm_f4 xs = *(const fm_f4 *)&cs.xsum[gg][4 * kq];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    acc[v] = __builtin_fmaf(scg, dg[v], __builtin_fmaf(big, xs[v], acc[v]));
+                    acc2[v] = __builtin_fmaf(scu, du[v], __builtin_fmaf(biu, xs[v], acc2[v]));
+                }
+                if (k & 1) __builtin_amdgcn_sched_barrier(0);  // bound the read-ahead (registers)
+            }
+        }
+    };
+    // Ring of R pieces with static slots: the step loop is unrolled by R, so
+    // no register ever moves between slots (a move would wait for the slot's
+    // loads) and every step issues the same loads -- the in-order wait counts
+    // stay exact and R - 1 pieces stay in flight while one is computed.
+    constexpr int R = pf_ring(NST);
     PfPiece<BITS> ring[R], ring2[DUAL ? R : 1];
     if constexpr (RES) {
         // resident operands: the stages hold the whole input, loaded once
-        // (before the weights: piece 0 needs them as early as its weights)
+        // (before the weights: piece 0 needs them as early as its weights).
+        // Outputs are stored after the step loop: gfx9 counts loads and
+        // stores in one counter, and a store pending anywhere in the loop
+        // turns every wait for a weight piece into a full drain (vmcnt(0))
+        // instead of "all but the younger ring slots".  Finished row tiles
+        // wait in a register bank.
+        constexpr int RT = pf_row_tiles(true, NST);
+        fm_f4v acc = (fm_f4v){0.f, 0.f, 0.f, 0.f}, acc2 = acc, bank[RT], bank2[DUAL ? RT : 1];
+#pragma unroll
+        for (int j = 0; j < RT; j++) bank[j] = acc;
+#pragma unroll
+        for (int j = 0; j < (DUAL ? RT : 1); j++) bank2[j] = acc;
         PfStageRegs<LO, W> sr[NST];
 #pragma unroll
         for (int k = 0; k < NST; k++)
@@ -459,38 +535,47 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
             if (k < np) pf_stage_store<LO, W>(st[k], sr[k]);
         __syncthreads();
         FM_PF_MARK(1);
+        // nq is a multiple of R (the launch guarantees it): no step is
+        // conditional, so every path through the loop has the same loads in
+        // flight and each wait leaves the younger ring slots outstanding
         for (int q0 = 0; q0 < nq; q0 += R) {
 #pragma unroll
             for (int i = 0; i < R; i++) {
                 const int q = q0 + i;
                 __builtin_amdgcn_sched_barrier(0);  // keep the unrolled steps apart (registers)
-                if (q < nq) {
-                    const int rt = q / np, pc = q - rt * np;
+                const int rt = q / np, pc = q - rt * np;
+                if constexpr (DUAL) {
+                    compute2(ring[i], ring2[i], st[pc], acc, acc2);
+                    load_piece(mat, q + R, ring[i]);
+                    load_piece(mat2, q + R, ring2[i]);
+                } else {
                     compute(ring[i], st[pc], acc);
                     load_piece(mat, q + R, ring[i]);
-                    if constexpr (DUAL) {
-                        compute(ring2[i], st[pc], acc2);
-                        load_piece(mat2, q + R, ring2[i]);
+                }
+                if (pc == np - 1) {  // row tile rt done: into the bank (tile k ends at RT - rl + k)
+#pragma unroll
+                    for (int j = 0; j + 1 < RT; j++) {
+                        bank[j] = bank[j + 1];
+                        if constexpr (DUAL) bank2[j] = bank2[j + 1];
                     }
-                    if (pc == np - 1) {
-                        emit(rt, acc, acc2);
-                        acc = (fm_f4v){0.f, 0.f, 0.f, 0.f};
-                        acc2 = acc;
-                    }
+                    bank[RT - 1] = acc;
+                    if constexpr (DUAL) bank2[RT - 1] = acc2;
+                    acc = acc2 = (fm_f4v){0.f, 0.f, 0.f, 0.f};
                 }
             }
         }
+#pragma unroll
+        for (int j = 0; j < RT; j++)
+            if (j >= RT - rl) emit(j - (RT - rl), bank[j], DUAL ? bank2[j] : bank[j]);
     } else {
-      if constexpr (NST == 2) {
+        static_assert(NST == 2 && !DUAL, "streamed operands: two stages, one matrix");
         // streamed operands: piece p + 1's stage registers go to LDS while
         // piece p + 2's are already loading; one barrier per piece
+        fm_f4v acc = (fm_f4v){0.f, 0.f, 0.f, 0.f};
         PfStageRegs<LO, W> sr[2];
         pf_stage_load<LO, W>(a, srow, xop, xlo, 0, sr[0]);
 #pragma unroll
-        for (int k = 0; k < R; k++) {
-            load_piece(mat, k, ring[k]);
-            if constexpr (DUAL) load_piece(mat2, k, ring2[k]);
-        }
+        for (int k = 0; k < R; k++) load_piece(mat, k, ring[k]);
         pf_stage_load<LO, W>(a, srow, xop, xlo, (uint32_t)min(1, np - 1) * PF_GPP, sr[1]);
         pf_stage_store<LO, W>(st[0], sr[0]);
         __syncthreads();
@@ -505,17 +590,12 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
                     compute(ring[i], st[i & 1], acc);
                     if (p == 0) FM_PF_MARK(2);
                     load_piece(mat, p + R, ring[i]);
-                    if constexpr (DUAL) {
-                        compute(ring2[i], st[i & 1], acc2);
-                        load_piece(mat2, p + R, ring2[i]);
-                    }
                     if (p + 1 < np) pf_stage_store<LO, W>(st[(i + 1) & 1], sr[(i + 1) & 1]);
                     __syncthreads();
                 }
             }
         }
-        emit(0, acc, acc2);
-      }
+        emit(0, acc, acc);
     }
     FM_PF_MARK(3);
 }
@@ -523,17 +603,18 @@ __device__ void pf_block(const PfArgs &a, const PfMat &mat, const PfMat &mat2, i
 // grid: one block per (chunk, matrix, row block) unit of max_chunks chunks;
 // units are consecutive chunks first, so the blocks that read the same
 // weights for consecutive chunks run side by side
-// W waves per workgroup (16 rows each): 4 for the two-stage kernels (two
-// workgroups per CU), 8 for the eight-stage gate/up kernel (one per CU).
-// RES / VEC select one operand path and one scale-load path at compile time,
-// so the registers are sized for the path the launch takes.
+// W waves per workgroup (16 rows each): 4 for the two-stage kernels (three
+// workgroups per CU when resident), 8 for the eight-stage gate/up kernel (one
+// per CU).  RES / VEC select one operand path and one scale-load path at
+// compile time, so the registers are sized for the path the launch takes.
 template <bool LO, bool DUAL, int NST, int W, bool RES, bool VEC>
-__global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_pf_gemm_kernel(PfArgs a) {
+__global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO || !RES ? 2 : PF_MINB)) void fm_pf_gemm_kernel(PfArgs a) {
     __shared__ PfStage<LO> st[NST];
     __shared__ uint32_t tbuf[W][16 * PF_TS];
     __shared__ int srow_s[PF_TOK], slot_s[PF_TOK];
     __shared__ float tinv_s[PF_TOK];  // each token column's 2^(24 - e)
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    FM_PF_MARK(5);
     // Units are (chunk, matrix, row block) over the LIVE chunks only (the grid is
     // sized for max_chunks; surplus blocks exit).  XCD-aware order: the 8 XCDs
     // take blocks round-robin, so XCD x gets the contiguous eighth x of the
@@ -541,7 +622,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
     // units) share that XCD's L2 instead of fetching the weights once per XCD.
     // mode 0 without DUAL: gate and up rows are separate units (matrix = mat)
     const uint32_t nmat = (a.mode == 0 && !DUAL) ? 2 : 1;
-    const int rl_big = pf_row_tiles(a.in_dim, NST);
+    const int rl_big = pf_row_tiles(RES, NST);
     const uint32_t rows_per_wg = 16 * W * rl_big;
     const uint32_t nrb = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
     const uint32_t nch = (uint32_t)*a.nchunks;
@@ -549,8 +630,11 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
     // Eight-stage kernel (one workgroup per CU, long units): the units of an
     // XCD's last partial round run as single row tiles, so that round ends
     // after about one row tile instead of one whole unit (the grid has room
-    // for the extra workgroups; the others exit).
-    const uint32_t full = (NST == 8 && rl_big > 1) ? per_xcd / a.xcd_slots * a.xcd_slots : per_xcd;
+    // for the extra workgroups; the others exit).  Single row tiles need a
+    // piece count that fills whole ring turns.
+    const uint32_t np = (a.in_dim / 64 + PF_GPP - 1) / PF_GPP;
+    const uint32_t full =
+        (NST == 8 && rl_big > 1 && np % pf_ring(NST) == 0) ? per_xcd / a.xcd_slots * a.xcd_slots : per_xcd;
     const uint32_t nsplit = (per_xcd - full) * (uint32_t)rl_big;
     const uint32_t lb = blockIdx.x / 8;
     uint32_t u, tile0 = 0;
@@ -581,6 +665,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO ? 2 : PF_MINB)) void fm_
         tinv_s[ei] = sr < 0 ? 0.f : a.xinv[sr];
     }
     __syncthreads();
+    FM_PF_MARK(6);
     int bits = 4;
     // mode 0: gate (matrix 0) and up (matrix 1) rows together
     const PfMat m = pf_mat(a, e, a.mode == 0 ? (int)mat : (a.mode == 1 ? 2 : 0), blob, cbits, bits);
@@ -891,16 +976,17 @@ static int pf_launch_gemm(PfArgs &a, bool lo, hipStream_t st) {
     const bool dual = !lo && a.mode == 0 && pf_dual(a.in_dim);
     const int nst = dual ? 8 : 2;
     const int W = dual ? 8 : 4;
-    const uint32_t rows_per_wg = 16 * W * pf_row_tiles(a.in_dim, nst);
+    const bool res = dual || np <= 2;  // operands resident in the stages
+    const uint32_t rows_per_wg = 16 * W * pf_row_tiles(res, nst);
     const uint32_t rowblocks = (a.out_dim + rows_per_wg - 1) / rows_per_wg;
     const uint32_t nmat = (a.mode == 0 && !dual) ? 2 : 1;
     // whole multiple of 8 blocks (the XCD-aware unit order), room for the
     // eight-stage kernel's split last round; extra blocks exit
     const size_t units = (size_t)a.max_chunks * rowblocks * nmat;
     a.xcd_slots = (uint32_t)((fm_num_cus() + 7) / 8);
-    const size_t per_xcd = (units + 7) / 8 + (dual ? (size_t)a.xcd_slots * (pf_row_tiles(a.in_dim, 8) - 1) : 0);
+    const size_t per_xcd = (units + 7) / 8 + (dual ? (size_t)a.xcd_slots * (pf_row_tiles(true, 8) - 1) : 0);
     dim3 grid((unsigned)(per_xcd * 8)), block(64 * W);
-    const bool res = np <= 2, vec = G % PF_GPP == 0;  // two-stage kernels: resident / vector-scale paths
+    const bool vec = G % PF_GPP == 0;  // a piece's scales are one 16-byte run
 #define PF_GO(LO_, R_, V_) hipLaunchKernelGGL((fm_pf_gemm_kernel<LO_, false, 2, 4, R_, V_>), grid, block, 0, st, a)
 #define PF_GO4(LO_)                      \
     if (res && vec) PF_GO(LO_, true, true);  \
