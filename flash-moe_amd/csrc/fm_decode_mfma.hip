@@ -699,12 +699,13 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
 // three work items (item = A tile + B tile of one slot, as above; item i of
 // workgroup g is g + i * grid).  A CU's vector memory requests are served in
 // issue order, so one workgroup per CU decides that order itself:
-//   x (once per CU, not once per item), then every item's gate/up rows, then
-//   every item's down rows -- all issued before any compute.
-// The gate/up bytes thus arrive first everywhere, the activations they feed
-// are published while the down bytes are still streaming, and the last bytes
-// a CU receives are down rows whose activations are (mostly) ready: the tail
-// after the stream is one hand-off plus the combine.  Slot descriptors come
+//   x (once per CU, not once per item), then every item's gate/up rows (the
+//   issue itself blocks while the CU's request queue is full: the last item's
+//   waves finish issuing ~9 us in), then each item's down rows as soon as its
+//   own activations are published -- the last item's copied into LDS by item
+//   0's waves at that point, ahead of the other items' down rows.
+// The gate/up bytes thus arrive first everywhere, and the down bytes stream
+// while the slots' activations are still being completed.  Slot descriptors come
 // from wave-uniform scalar loads (idx -> pool tables), which do not queue
 // behind the vector stream.  The four waves of an item synchronise through an
 // LDS counter, so items progress independently of each other.
@@ -725,14 +726,34 @@ struct __attribute__((aligned(16))) FmcItem {
     uint32_t sync;                // the item's 4-wave barrier counter
 };
 
+#ifndef FMC_DN_LDS
+#define FMC_DN_LDS 1  // the last item's down rows copied into LDS early (see fm_decode_cu_kernel)
+#endif
+
 struct __attribute__((aligned(16))) FmcLds {
     fm_h2 xq[2][FMM_GH][32];
     fm_h2 zero[32];
     float xsum[FMM_GH];
     float xinv[FMM_GH];
     uint32_t xready;              // count of item 0's waves that built the x operands
+    uint32_t dn_ready;            // count of item 0's waves whose copy of the last item's down rows landed
     FmcItem it[FMC_NG];
+    uint32_t dn[4][16 * FMM_MAXI / 8];     // last item: each wave's 16 down rows (4-bit: 128 words a row)
+    uint16_t dsb[4][2][16 * FMM_GI];       // ... and their scales / biases
 };
+
+// Copy 16-byte runs into LDS with the vector memory DMA path (lane l's run
+// lands at lds + 16 l).  Written as inline assembly so that the compiler's
+// wait counts ignore it: they then only ever over-wait (these loads are older
+// than every load it counts after them), and the issuing wave waits for the
+// copy itself with an explicit vmcnt.  m0 (the DMA's LDS base) is restored.
+FM_DEV void fmc_dma16(void *lds, const void *g) {
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "s"((uint32_t)(uintptr_t)lds), "v"(g)
+                 : "memory");
+}
 
 typedef __attribute__((address_space(4))) const uint32_t fmc_cu32;
 typedef __attribute__((address_space(4))) const uint64_t fmc_cu64;
@@ -807,7 +828,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     FM_DX_MARK(0);
     // counters first (no load is in flight yet, so this barrier is cheap)
     if (tid < FMC_NG) L.it[tid].sync = 0;
-    if (tid == 0) L.xready = 0;
+    if (tid == 0) L.xready = L.dn_ready = 0;
     __syncthreads();
     const uint32_t ep_ld = fm_epoch_load(a);
     // x: every wave loads elements 16 t .. 16 t + 15 of its item-relative
@@ -818,6 +839,14 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (gt < (int)GH * 4 ? gt : 0) + 4 * j);
     const FmSlot s = fmc_slot(a, k);
     const bool doA = has && s.valid;
+    // The last item's down rows: item 0's waves copy them into LDS right
+    // after publishing their own activations, so they queue behind the gate/up
+    // stream instead of behind the last item's own activation wait.
+    const uint32_t item_l = blockIdx.x + gridDim.x * (uint32_t)(FMC_NG - 1);
+    const bool has_l = item_l < (uint32_t)a.S * TILES;
+    const int k_l = has_l ? (int)(item_l / TILES) : 0;
+    const FmSlot s_l = (FMC_DN_LDS && grp == 0) ? fmc_slot(a, k_l) : s;
+    const bool dn_lds = FMC_DN_LDS && (grp == 0 ? has_l && s_l.valid : (grp == FMC_NG - 1 && doA));
     // Every gate/up load of the item.  Loads issue in order and block while
     // the CU's request queue is full, so a wave issues its down rows only
     // after its activations are published (a blocked issue would hold back
@@ -951,9 +980,32 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         const float u = (T.part[0][gt][1] + T.part[1][gt][1]) + (T.part[2][gt][1] + T.part[3][gt][1]);
         fm_put_tagged(&a.act2[(size_t)k * I + rowA0 + gt], fm_silu_mul(g, u), ep);
     }
-    // the down rows (queue behind every gate/up request of the CU)
-    fmm_issue_codes<NG>(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
-    fmm_issue_sb<NG>(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
+    if (dn_lds && grp == 0) {
+        // wave wv copies the last item's wave wv rows: 16 rows x (NG groups x
+        // 2 bits words), contiguous, then their scales and biases (NG x 2
+        // bytes a row)
+        const int bl = s_l.bits;
+        const uint32_t rows0 = (item_l % TILES) * 64 + 16 * wv, wpr = NG * 2 * bl;
+        const char *src = (const char *)(s_l.dw + (size_t)rows0 * wpr);
+        const int runs = 16 * wpr * 4 / 1024;  // 1 KB per instruction
+        for (int r = 0; r < runs; r++) fmc_dma16(&L.dn[wv][256 * r], src + 1024 * r + 16 * lane);
+        if (lane < NG * 2) {  // 16 rows x NG bf16 = 32 NG bytes
+            fmc_dma16(&L.dsb[wv][0][0], (const char *)(s_l.ds + (size_t)rows0 * NG) + 16 * lane);
+            fmc_dma16(&L.dsb[wv][1][0], (const char *)(s_l.db + (size_t)rows0 * NG) + 16 * lane);
+        }
+    }
+    // the down rows (queue behind every gate/up request of the CU); the last
+    // item's come from LDS (its loads read the dummy, so the count of loads in
+    // flight is the same on every path)
+    const bool dn_glob = doA && !(dn_lds && grp == FMC_NG - 1);
+    fmm_issue_codes<NG>(s.dw, bits, rowB0, I, 0, dn_glob, cdn, lane, a.x);
+    fmm_issue_sb<NG>(s.ds, s.db, rowB0, I, 0, dn_glob, sdn, bdn, lane, a.x);
+    if (dn_lds && grp == 0) {
+        // the copy is older than the NG / 2 + 2 loads just issued
+        static_assert(NG / 2 + 2 <= 15, "vmcnt immediate");
+        __builtin_amdgcn_s_waitcnt((NG / 2 + 2) | (0x7 << 4) | (0xF << 8));
+        if (lane == 0) __hip_atomic_fetch_add(&L.dn_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     FM_DX_MARK(4);
 
     // ---- B: the slot's activations (every A tile of the slot), then 16 down rows per wave ----
@@ -998,6 +1050,29 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     }
     fmc_item_sync(&T.sync, phase);
     FM_DX_MARK(5);
+    if (dn_lds && grp == FMC_NG - 1) {
+        // this item's down rows from LDS, in the lane layout of fmm_issue_codes / fmm_issue_sb
+        uint32_t it = 0;
+        while (__hip_atomic_load(&L.dn_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 4 && ++it < FM_SPIN_MAX)
+            __builtin_amdgcn_s_sleep(1);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+        asm volatile("" ::: "memory");
+        const uint32_t wpr = NG * 2 * s.bits;
+        const int nw = (NG == 8 && s.bits == 2) ? (n & 7) : n;
+#pragma unroll
+        for (int p = 0; p < NG / 8; p++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t po = s.bits == 4 ? 64 * p : 0;
+                cdn.c[4 * p + j] = *(const fm_u4 *)&L.dn[wv][(4 * j + q) * wpr + po + 4 * nw];
+            }
+        if (4 * q < NG) {
+            sdn = *(const fmm_u2 *)&L.dsb[wv][0][n * NG + 4 * q];
+            bdn = *(const fmm_u2 *)&L.dsb[wv][1][n * NG + 4 * q];
+        } else {
+            sdn = bdn = (fmm_u2){0u, 0u};
+        }
+    }
     if (doA) {
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &T.aq[s.bits == 4 ? 0 : 1][0][0];
