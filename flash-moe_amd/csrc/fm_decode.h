@@ -51,6 +51,14 @@ struct FmDecodeArgs {
     float *normed;           // fp32 [hidden]
     uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
     uint64_t *p2;            // few-slot kernel: [S][64 tiles][4 quarters][16 rows][gate, up] tagged partials
+    // routing fused into the step (one token, pool mode, one-workgroup-per-CU
+    // kernel): softmax / top-K / renormalise of route_logits in every
+    // workgroup; idx / wdev are then unused, and the slot-order indices and
+    // weights of cpu_topk / cpu_normalize_weights go to route_idx / route_w
+    const float *route_logits;  // [route_E] or NULL (routing done by the caller)
+    int route_E;
+    int *route_idx;             // [K] out
+    float *route_w;             // [K] out
 };
 
 // Slot k of token tok (routed slots of token tok read idx/wdev row tok).

@@ -801,6 +801,18 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     a.p2 = (uint64_t *)p;
     a.ws_epoch = (uint32_t *)((char *)ws + FM_WS_EPOCH_OFF);
     a.ws_done = (uint32_t *)((char *)ws + FM_WS_DONE_OFF);
+    if (a.route_logits) {
+        // routing fused into the step where the per-CU kernel runs it;
+        // otherwise the routing kernel first, then the step on its outputs
+        int rc = fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st) : FM_ERR_UNSUPPORTED;
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
+        rc = fm_route_topk(a.route_logits, 1, a.route_E, a.K, a.route_idx, a.route_w, st);
+        if (rc) return rc;
+        a.route_logits = nullptr;
+        a.idx = a.route_idx;
+        a.wdev = a.route_w;
+    }
     if (a.ntok > 1)  // several tokens in one launch: only the mfma kernel implements it
         return fm_decode_allowed("mfma") ? fm_launch_decode_mfma(a, st)
                                          : fm_fail(FM_ERR_UNSUPPORTED, "%s: several tokens need the mfma kernel", who);
@@ -936,7 +948,8 @@ static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int 
                                const float *weights, const fm_expert_weights *shared, int shared_bits,
                                uint32_t shared_inter, const float *shared_gate_score, const float *x, const float *h_mid, float *out,
                                uint16_t *out_bf16, const uint16_t *norm_w, float norm_eps, float *normed, void *ws,
-                               size_t ws_bytes, void *stream, int T = 1) {
+                               size_t ws_bytes, void *stream, int T = 1, const float *route_logits = nullptr,
+                               int route_E = 0) {
     FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
     FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
     FM_REQUIRE(K == 0 || (idx && weights), "%s: NULL idx/weights", who);
@@ -977,6 +990,12 @@ static int fm_decode_pool_impl(const char *who, const fm_expert_pool *pool, int 
     a.h_mid = h_mid;
     a.out = out;
     a.out_bf16 = out_bf16;
+    if (route_logits) {
+        a.route_logits = route_logits;
+        a.route_E = route_E;
+        a.route_idx = const_cast<int *>(idx);
+        a.route_w = const_cast<float *>(weights);
+    }
     if (T > 1) {
         if (fm_shared_apart(K, a.has_shared, a.inter, shared_inter))
             return fm_fail(FM_ERR_UNSUPPORTED, "%s: several tokens with a shared expert of its own size", who);
@@ -1007,6 +1026,22 @@ extern "C" int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *
     return fm_decode_pool_impl("fm_moe_decode_pool", pool, K, idx, weights, shared, shared_bits, shared_inter,
                                shared_gate_score, x,
                                h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream);
+}
+
+extern "C" int fm_moe_route_decode_pool(const fm_expert_pool *pool, const float *logits, int E, int K, int *idx,
+                                        float *weights, const fm_expert_weights *shared, int shared_bits,
+                                        uint32_t shared_inter, const float *shared_gate_score, const float *x,
+                                        const float *h_mid, float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
+                                        void *stream) {
+    const char *who = "fm_moe_route_decode_pool";
+    fm_clear_error();
+    FM_REQUIRE(logits && idx && weights, "%s: NULL logits/idx/weights", who);
+    FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
+    FM_REQUIRE(K >= 1 && K <= FM_MAX_K, "%s: K=%d outside 1..%d", who, K, FM_MAX_K);
+    FM_REQUIRE(E >= K && E <= 4096 && (uint32_t)E <= pool->num_experts,
+               "%s: E=%d outside K..min(4096, pool experts %u)", who, E, pool->num_experts);
+    return fm_decode_pool_impl(who, pool, K, idx, weights, shared, shared_bits, shared_inter, shared_gate_score, x,
+                               h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream, 1, logits, E);
 }
 
 // ------------------------------------------------- no-allocation variant --

@@ -33,6 +33,7 @@
 // is in flight from the first microsecond; down-projection loads follow once
 // the wave's own gate/up work is done.
 #include "fm_decode.h"
+#include "fm_route_dev.h"
 
 #include <stdlib.h>
 
@@ -730,6 +731,18 @@ struct __attribute__((aligned(16))) FmcItem {
 #define FMC_DN_LDS 1  // the last item's down rows copied into LDS early (see fm_decode_cu_kernel)
 #endif
 
+// Routing fused into the step (FmDecodeArgs::route_logits): scratch of the
+// prologue, and of the one wavefront that writes the slot-order outputs.
+struct __attribute__((aligned(16))) FmcRoute {
+    int pb[FMC_THREADS];              // probability bits, -2 past E (whole 64-element chunks)
+    int cv[FMC_THREADS + 4];          // top-K candidates: probability bits
+    int ci[FMC_THREADS + 4];          // ... and element indices
+    float red[2][FMC_THREADS / 64];   // per-wave max / sum
+    int ncand, straddle, vk;
+    float s_val[64];                  // cpu_topk slots (serial replay)
+    int s_id[64];
+};
+
 struct __attribute__((aligned(16))) FmcLds {
     fm_h2 xq[2][FMM_GH][32];
     fm_h2 zero[32];
@@ -738,8 +751,17 @@ struct __attribute__((aligned(16))) FmcLds {
     uint32_t xready;              // count of item 0's waves that built the x operands
     uint32_t dn_ready;            // count of item 0's waves whose copy of the last item's down rows landed
     FmcItem it[FMC_NG];
-    uint32_t dn[4][16 * FMM_MAXI / 8];     // last item: each wave's 16 down rows (4-bit: 128 words a row)
+    union {
+        // the routing scratch is dead once every wave has passed the
+        // prologue; the down-row copy starts later (after item 0's
+        // activations), and never on the CU whose idle wave group writes
+        // the slot-order outputs (it holds no last item)
+        uint32_t dn[4][16 * FMM_MAXI / 8];     // last item: each wave's 16 down rows (4-bit: 128 words a row)
+        FmcRoute rt;
+    };
     uint16_t dsb[4][2][16 * FMM_GI];       // ... and their scales / biases
+    int rsel[FM_MAX_K];           // fused routing: expert of routed slot k (descending probability)
+    int rp[FM_MAX_K];             // ... and its probability bits
 };
 
 // Copy 16-byte runs into LDS with the vector memory DMA path (lane l's run
@@ -763,12 +785,21 @@ FM_DEV uint32_t fmc_ld32(const void *p) { return *(fmc_cu32 *)p; }
 FM_DEV uint64_t fmc_ld64(const void *p) { return *(fmc_cu64 *)p; }
 
 // Slot k (wave-uniform) resolved with scalar loads: idx / weight, then the
-// pool's blob address and bit width.
-FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k) {
+// pool's blob address and bit width.  With rsel (fused routing) the expert
+// and its probability come from LDS and the weight is p * winv.
+FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k, const int *rsel = nullptr, const int *rp = nullptr,
+                       float winv = 1.f) {
     if (!a.pool_mode || k >= a.K) return a.slot[k];
     FmSlot s;
-    const int e = (int)fmc_ld32(a.idx + k);
-    const float w = __uint_as_float(fmc_ld32(a.wdev + k));
+    int e;
+    float w;
+    if (rsel) {
+        e = __builtin_amdgcn_readfirstlane(rsel[k]);
+        w = __int_as_float(__builtin_amdgcn_readfirstlane(rp[k])) * winv;
+    } else {
+        e = (int)fmc_ld32(a.idx + k);
+        w = __uint_as_float(fmc_ld32(a.wdev + k));
+    }
     if (e < 0 || (uint32_t)e >= a.pool_n) {
         s.valid = 0;
         s.bits = 4;
@@ -794,6 +825,146 @@ FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k) {
     return s;
 }
 
+// Routing of one token in every workgroup of the one-workgroup-per-CU kernel
+// (FmDecodeArgs::route_logits): cpu_softmax / cpu_topk / cpu_normalize_weights
+// (cpu_kernels.h:263-309).  Thread t holds logit t (E <= FMC_THREADS).
+//  * softmax with the arithmetic of fm_route_kernel (same per-wave sums, added
+//    in wave order; the waves past E add zeros), so the probabilities are
+//    bit-equal to that kernel's;
+//  * the top-K SET: any element of the K largest lies at or above the K-th
+//    largest of its own 64-element chunk, so the chunk lower bounds of
+//    fm_kth_lower_bound keep ~K candidates a chunk; each candidate counts the
+//    candidates ahead of it (larger, or equal with a lower index).  Unless a
+//    run of equal probabilities straddles the K-th place, the K largest are
+//    exactly cpu_topk's slots (a strictly larger newcomer is needed to evict,
+//    and it can only evict an element with K others at or above it); with a
+//    straddling tie wavefront 0 replays cpu_topk (fm_topk_serial), which
+//    settles which of the equal elements stay.
+// L.rsel / L.rp receive the set in descending order (the kernel's slot order:
+// only the order of the weighted sum differs from cpu_topk's slots, a
+// rounding-level difference); returns 1 / sum of the selected probabilities,
+// the renormalisation factor (computed by every wave alike).
+FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int E = a.route_E, K = a.K, nch = (E + 63) >> 6;
+    constexpr int NW = FMC_THREADS / 64;
+    FmcRoute &R = L.rt;
+    // every wave holds all E logits (lane l: elements l, 64 + l, ...): the
+    // max needs no exchange between waves; the per-wave sums do
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NW; q++) mx = fmaxf(mx, lgq[q]);
+    mx = fm_wave_max(mx);
+    FM_DX_MARK(8);
+    float lg = lgq[0];
+#pragma unroll
+    for (int q = 1; q < NW; q++) lg = wv == q ? lgq[q] : lg;
+    const float ev = tid < E ? expf(lg - mx) : 0.f;
+    const float ws = fm_lane_sum<64>(ev);
+    if (lane == 0) R.red[1][wv] = ws;
+    __syncthreads();
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) sum += R.red[1][w];
+    const float inv = 1.0f / sum;
+    const int pv = tid < E ? __float_as_int(ev * inv) : -2;
+    FM_DX_MARK(9);
+    if (tid < nch * 64) R.pb[tid] = pv;
+    if (wv < nch) {
+        const int res = fm_kth_lower_bound(pv, K);
+        const uint64_t m = __ballot(pv >= res);
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&R.ncand, __builtin_popcountll(m));
+        base = __builtin_amdgcn_readlane(base, 0);
+        if ((m >> lane) & 1ull) {
+            const int pos = base + fm_mbcnt(m);
+            R.cv[pos] = pv;
+            R.ci[pos] = tid;
+        }
+    }
+    __syncthreads();
+    FM_DX_MARK(10);
+    const int NC = R.ncand;
+    if (NC <= FMC_THREADS / 8) {
+        // eight lanes per candidate (lane r: entries 12 r .. 12 r + 11); a
+        // candidate's place = the number of candidates ahead of it by the key
+        // (probability bits, then the lower index first), counted on 64-bit
+        // keys, summed over the 8 lanes (quad_perm [1,0,3,2], [2,3,0,1],
+        // row_half_mirror).  Places K-1 and K then tell whether a run of
+        // equal probabilities straddles the K-th place.
+        const int c = tid >> 3, r = tid & 7;
+        const bool act = c < NC;
+        const uint64_t key = act ? ((uint64_t)(uint32_t)R.cv[c] << 32) | (uint32_t)(1023 - R.ci[c]) : 0;
+        int cnt = 0;
+        if (act) {
+            int4 cv4[3], ci4[3];
+#pragma unroll
+            for (int h = 0; h < 3; h++) {
+                cv4[h] = *reinterpret_cast<const int4 *>(&R.cv[12 * r + 4 * h]);
+                ci4[h] = *reinterpret_cast<const int4 *>(&R.ci[12 * r + 4 * h]);
+            }
+#pragma unroll
+            for (int h = 0; h < 3; h++) {
+                const int cc[4] = {cv4[h].x, cv4[h].y, cv4[h].z, cv4[h].w};
+                const int dd[4] = {ci4[h].x, ci4[h].y, ci4[h].z, ci4[h].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint64_t kj = ((uint64_t)(uint32_t)cc[q] << 32) | (uint32_t)(1023 - dd[q]);
+                    cnt += (12 * r + 4 * h + q < NC && kj > key) ? 1 : 0;
+                }
+            }
+        }
+        cnt += fm_dpp_i<0xB1>(cnt);
+        cnt += fm_dpp_i<0x4E>(cnt);
+        cnt += fm_dpp_i<0x141>(cnt);
+        if (act && r == 0) {
+            if (cnt < K) {
+                L.rsel[cnt] = (int)(1023 - (uint32_t)key);
+                L.rp[cnt] = (int)(key >> 32);
+            } else if (cnt == K) {
+                R.vk = (int)(key >> 32);  // the first probability left out
+            }
+        }
+    } else if (tid < NC) {
+        const int v = R.cv[tid], me = R.ci[tid];
+        int gt = 0, ahead = 0, eq = 0;
+        for (int j = 0; j < NC; j += 4) {
+            const int4 c = *reinterpret_cast<const int4 *>(&R.cv[j]);
+            const int4 d = *reinterpret_cast<const int4 *>(&R.ci[j]);
+            const int cc[4] = {c.x, c.y, c.z, c.w}, dd[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const bool in = j + q < NC;
+                gt += in && cc[q] > v;
+                eq += in && cc[q] == v;
+                ahead += in && cc[q] == v && dd[q] < me;
+            }
+        }
+        const int pos = gt + ahead;
+        if (pos < K) {
+            L.rsel[pos] = me;
+            L.rp[pos] = v;
+        }
+        if (gt < K && gt + eq > K) R.straddle = 1;
+    }
+    __syncthreads();
+    FM_DX_MARK(11);
+    if (R.straddle || (NC <= FMC_THREADS / 8 && R.vk == L.rp[K - 1])) {  // uniform: read after the barrier
+        if (wv == 0) {
+            fm_topk_serial(R.pb, E, K, R);
+            fm_wave_lds_sync();
+            if (lane < K) {
+                L.rsel[lane] = R.s_id[lane];
+                L.rp[lane] = __float_as_int(R.s_val[lane]);
+            }
+        }
+        __syncthreads();
+    }
+    float s = 0.f;
+    for (int k = 0; k < K; k++) s += __int_as_float(L.rp[k]);
+    return s > 0.f ? 1.0f / s : 1.0f;
+}
+
 // Barrier of the 4 waves of one item: an LDS counter that only grows (target
 // += 4 per use).  Waits on LDS operations only -- the item's weight loads stay
 // in flight across it.
@@ -810,7 +981,7 @@ FM_DEV void fmc_item_sync(uint32_t *ctr, uint32_t &target) {
 // NG = input groups of one wave's share of a row (16: hidden 4096 / inter 1024;
 // 8: hidden 2048 / inter 512).  hidden = 256 NG, inter = hidden / 4, so the
 // gate/up tiles (16 rows) and the down tiles (64 rows) of a slot pair up.
-template <int NG>
+template <int NG, bool RT>  // RT: routing fused into the launch (FmDecodeArgs::route_logits)
 __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeArgs a) {
     __shared__ FmcLds L;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -828,16 +999,32 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     FM_DX_MARK(0);
     // counters first (no load is in flight yet, so this barrier is cheap)
     if (tid < FMC_NG) L.it[tid].sync = 0;
-    if (tid == 0) L.xready = L.dn_ready = 0;
+    if (tid == 0) {
+        L.xready = L.dn_ready = 0;
+        if constexpr (RT) {
+            L.rt.ncand = L.rt.straddle = 0;  // fused routing: candidate count, tie flag
+            L.rt.vk = -1;                      // ... and the first probability left out (none)
+        }
+    }
     __syncthreads();
     const uint32_t ep_ld = fm_epoch_load(a);
+    constexpr bool fused = RT;
+    float lgq[FMC_THREADS / 64];
+    if constexpr (RT) {
+#pragma unroll
+        for (int q = 0; q < FMC_THREADS / 64; q++)
+            lgq[q] = 64 * q + lane < a.route_E ? a.route_logits[64 * q + lane] : -INFINITY;
+    }
     // x: every wave loads elements 16 t .. 16 t + 15 of its item-relative
     // thread t (items 1 and 2 hit the lines item 0 brings into the CU's
     // cache); item 0 turns them into operand rows below
     fm_f4 xr[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (gt < (int)GH * 4 ? gt : 0) + 4 * j);
-    const FmSlot s = fmc_slot(a, k);
+    float winv = 1.f;
+    if constexpr (RT) winv = fmc_route(a, L, lgq);
+    const int *rsel = RT ? L.rsel : nullptr;
+    const FmSlot s = fmc_slot(a, k, rsel, L.rp, winv);
     const bool doA = has && s.valid;
     // The last item's down rows: item 0's waves copy them into LDS right
     // after publishing their own activations, so they queue behind the gate/up
@@ -845,7 +1032,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     const uint32_t item_l = blockIdx.x + gridDim.x * (uint32_t)(FMC_NG - 1);
     const bool has_l = item_l < (uint32_t)a.S * TILES;
     const int k_l = has_l ? (int)(item_l / TILES) : 0;
-    const FmSlot s_l = (FMC_DN_LDS && grp == 0) ? fmc_slot(a, k_l) : s;
+    const FmSlot s_l = (FMC_DN_LDS && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv) : s;
     const bool dn_lds = FMC_DN_LDS && (grp == 0 ? has_l && s_l.valid : (grp == FMC_NG - 1 && doA));
     // Every gate/up load of the item.  Loads issue in order and block while
     // the CU's request queue is full, so a wave issues its down rows only
@@ -876,7 +1063,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
 #pragma unroll
         for (int kk = 0; kk < FM_MAX_SLOTS; kk++) {
             if (kk < a.S) {
-                const FmSlot sk = fmc_slot(a, kk);
+                const FmSlot sk = fmc_slot(a, kk, rsel, L.rp, winv);
                 if (lane == 0) L.it[grp].cw[kk] = sk.weight;
                 vm |= sk.valid ? 1u << kk : 0u;
             }
@@ -1161,9 +1348,24 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         }
     }
     FM_DX_MARK(7);
-    if (a.pool_mode && blockIdx.x == 0 && tid < a.K) {
+    if (a.pool_mode && !fused && blockIdx.x == 0 && tid < a.K) {
         const int e = a.idx[tid];
         if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
+    }
+    if (fused && blockIdx.x == gridDim.x - 1 && grp == FMC_NG - 1 && wv == 0) {
+        // the idle wave group of the last CU (the launch guarantees it holds
+        // no item, so its CU makes no down-row copy over the routing scratch):
+        // cpu_topk's slot order by serial replay, then cpu_normalize_weights
+        // (sequential sum over the slots) -- bit-equal to fm_route_kernel
+        fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt);
+        fm_wave_lds_sync();
+        if (lane < a.K) {
+            float sm = 0.f;
+            for (int kk = 0; kk < a.K; kk++) sm += L.rt.s_val[kk];
+            const float v = L.rt.s_val[lane];
+            a.route_idx[lane] = L.rt.s_id[lane];
+            a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
+        }
     }
     // Publishing the next epoch.  With the last slot valid, the combining
     // item of tile 0 has, through its waits, observed every tag user: each
@@ -1420,21 +1622,34 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     FM_DX_MARK(7);
 }
 
+// Fused routing needs the one-workgroup-per-CU kernel with the last CU's
+// third wave group idle (it writes the slot-order outputs), one logit per
+// thread, and the combine.
+static bool fmc_route_fits(const FmDecodeArgs &a, uint32_t tiles, int cus) {
+    return a.ntok <= 1 && a.mode == 0 && a.pool_mode && a.K >= 1 && a.K <= 64 && a.route_E >= a.K &&
+           a.route_E <= FMC_THREADS && (uint32_t)a.S * tiles <= (uint32_t)(FMC_NG * cus) - 1;
+}
+
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
     const int cus = fm_num_cus();
+    if (a.route_logits && !fmc_route_fits(a, a.hidden / 64, cus))
+        return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: fused routing does not fit this launch");
     // hidden 2048 / inter 512 (the Qwen3.5-35B-A3B expert shape): the
     // one-workgroup-per-CU kernel with 8-group units, one token whose items
     // fit three per CU
     if (a.hidden == 2048 && a.inter == 512) {
         static int per_cu_8 = -1;
         if (per_cu_8 < 0 &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_8, fm_decode_cu_kernel<8>, FMC_THREADS, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_8, fm_decode_cu_kernel<8, false>, FMC_THREADS, 0) !=
                 hipSuccess)
             per_cu_8 = 0;
         if (a.ntok <= 1 && a.spt == a.S && per_cu_8 >= 1 && (uint32_t)a.S * 32 <= (uint32_t)(FMC_NG * cus) &&
             a.S <= FM_MAX_SLOTS) {
-            hipLaunchKernelGGL(fm_decode_cu_kernel<8>, dim3(cus), dim3(FMC_THREADS), 0, st, a);
+            if (a.route_logits)
+                hipLaunchKernelGGL((fm_decode_cu_kernel<8, true>), dim3(cus), dim3(FMC_THREADS), 0, st, a);
+            else
+                hipLaunchKernelGGL((fm_decode_cu_kernel<8, false>), dim3(cus), dim3(FMC_THREADS), 0, st, a);
             return fm_check_launch("fm_decode_cu_kernel");
         }
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: 2048/512 takes one token");
@@ -1454,7 +1669,7 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
     // up to four slots of one token (no fused norm): the split kernel
-    if (a.ntok <= 1 && a.S <= FMS_MAXS && !a.norm_w) {
+    if (a.ntok <= 1 && a.S <= FMS_MAXS && !a.norm_w && !a.route_logits) {
         const char *no_split = getenv("FMOE_DECODE_NO_SPLIT");
         if (!(no_split && *no_split)) {
             hipLaunchKernelGGL(fm_decode_split_kernel, dim3(FMS_GRID), dim3(256), 0, st, a);
@@ -1463,7 +1678,7 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     }
     static int per_cu_c = -1;
     if (per_cu_c < 0 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel<16>, FMC_THREADS, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_c, fm_decode_cu_kernel<16, false>, FMC_THREADS, 0) != hipSuccess)
         per_cu_c = 0;
     // one token whose items fit three per CU: the one-workgroup-per-CU kernel
     // (FMOE_DECODE_NO_CU set in the environment: the three-workgroup kernel,
@@ -1471,9 +1686,13 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     const char *no_cu = getenv("FMOE_DECODE_NO_CU");
     if (a.ntok <= 1 && per_cu_c >= 1 && (uint32_t)a.S * (FMM_H / 64) <= (uint32_t)(FMC_NG * cus) &&
         a.S <= FM_MAX_SLOTS && !(no_cu && *no_cu)) {
-        hipLaunchKernelGGL(fm_decode_cu_kernel<16>, dim3(cus), dim3(FMC_THREADS), 0, st, a);
+        if (a.route_logits)
+            hipLaunchKernelGGL((fm_decode_cu_kernel<16, true>), dim3(cus), dim3(FMC_THREADS), 0, st, a);
+        else
+            hipLaunchKernelGGL((fm_decode_cu_kernel<16, false>), dim3(cus), dim3(FMC_THREADS), 0, st, a);
         return fm_check_launch("fm_decode_cu_kernel");
     }
+    if (a.route_logits) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: fused routing needs the per-CU kernel");
     const uint32_t tiles = a.inter / 16 > a.hidden / 64 ? a.inter / 16 : a.hidden / 64;
     const uint32_t items = (uint32_t)a.S * tiles;
     // every block may wait on others: the grid must be resident, and it is a

@@ -85,12 +85,12 @@ FM_DEV void fm_wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Serial replay on wavefront 0 (fallback): exact for ties.  The K slot keys
+// Serial replay on one wavefront (fallback): exact for ties.  The K slot keys
 // are kept sorted across lanes (lane 0 = the minimum, lowest slot first among
 // equal values); an insertion shifts the smaller keys down one lane.
 template <class LDS>
 __device__ void fm_topk_serial(const int *pb, int E, int K, LDS &L) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     int kval = lane < K ? -1 : 0x7fffffff;
     int kslot = lane < K ? lane : 64;
     int kid = 0;

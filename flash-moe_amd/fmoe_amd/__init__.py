@@ -91,6 +91,8 @@ SIGNATURES = {
                             I32, U32, F32, U32, U32, U32, P, P, P, P, P, SZ, P]),
     "fm_moe_decode_pool": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
                                  I32, U32, P, P, P, P, P, P, SZ, P]),
+    "fm_moe_route_decode_pool": (I32, [ctypes.POINTER(ExpertPool), P, I32, I32, P, P,
+                                       ctypes.POINTER(ExpertWeights), I32, U32, P, P, P, P, P, P, SZ, P]),
     "fm_moe_decode_pool_norm": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
                                       I32, U32, P, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),

@@ -17,7 +17,7 @@ __all__ = [
     "moe_prefill_forward", "moe_forward_workspace_bytes", "moe_prefill_workspace_bytes",
     "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
     "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS", "STATUS_EPOCH_WRAP", "workspace_init",
-    "workspace", "moe_decode_pool_noalloc", "decode_workspace_bytes_ex",
+    "workspace", "moe_decode_pool_noalloc", "decode_workspace_bytes_ex", "moe_route_decode_pool",
 ]
 
 STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP = 1, 2, 4, 8
@@ -94,6 +94,18 @@ def moe_decode_pool(pool, idx, weights, x, out, ws, shared=None, shared_bits=4, 
         ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
         shared_bits, shared_inter, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
         ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def moe_route_decode_pool(pool, logits, idx, weights, x, out, ws, shared=None, shared_bits=4, shared_score=None,
+                          h_mid=None, out_bf16=None, stream=None, shared_inter=0):
+    """Routing of `logits` ([E] or [1, E]) and the decode step in one launch
+    (fm_moe_route_decode_pool); idx / weights ([K]) receive the routing."""
+    K = idx.numel()
+    E = logits.numel()
+    check(lib().fm_moe_route_decode_pool(
+        ctypes.byref(pool.c), ptr(logits), E, K, ptr(idx), ptr(weights),
+        ctypes.byref(shared) if shared is not None else None, shared_bits, shared_inter, ptr(shared_score), ptr(x),
+        ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
 
 
 def moe_decode_pool_noalloc(pool, idx, weights, x, out, shared=None, shared_bits=4, shared_score=None,

@@ -204,6 +204,24 @@ int fm_moe_decode_pool(const fm_expert_pool *pool, int K, const int *idx,
                        const float *x, const float *h_mid, float *out,
                        uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
 
+/* Routing and the decode step in ONE launch: cpu_softmax / cpu_topk /
+ * cpu_normalize_weights of the E router logits (cpu_kernels.h:263-309, as
+ * called at layer_forward.h:3519-3523) followed by CMD3 (layer_forward.h:
+ * 3895-3993) on the selected pool experts -- fm_route_topk + fm_moe_decode_pool
+ * without the boundary between them.  logits: device fp32 [E]; idx / weights:
+ * device [K] OUTPUTS, written in cpu_topk's slot order (bit-equal to
+ * fm_route_topk).  K <= FM_MAX_K, E <= min(4096, pool experts).  The weighted
+ * sum of the step runs over the experts in descending probability (the output
+ * differs from fm_moe_decode_pool's only by rounding).  Where the fused kernel
+ * does not apply (E > 768, other shapes, no free wave group) it runs the two
+ * launches.  Workspace: fm_moe_decode_workspace_size_ex, as for
+ * fm_moe_decode_pool. */
+int fm_moe_route_decode_pool(const fm_expert_pool *pool, const float *logits, int E, int K, int *idx,
+                             float *weights, const fm_expert_weights *shared, int shared_bits,
+                             uint32_t shared_inter, const float *shared_gate_score, const float *x,
+                             const float *h_mid, float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
+                             void *stream);
+
 /* No counterpart in the reference: fm_moe_decode_pool for callers that cannot
  * allocate device memory (code recorded into a HIP graph, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments and result, minus the
