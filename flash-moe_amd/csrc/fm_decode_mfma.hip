@@ -734,11 +734,12 @@ struct __attribute__((aligned(16))) FmcItem {
 // Routing fused into the step (FmDecodeArgs::route_logits): scratch of the
 // prologue, and of the one wavefront that writes the slot-order outputs.
 struct __attribute__((aligned(16))) FmcRoute {
-    int pb[FMC_THREADS];              // probability bits, -2 past E (whole 64-element chunks)
+    int pb[FMC_THREADS];              // exp(l - max) bits (probability bits once pconv), -2 past E
     int cv[FMC_THREADS + 4];          // top-K candidates: probability bits
     int ci[FMC_THREADS + 4];          // ... and element indices
-    float red[2][FMC_THREADS / 64];   // per-wave max / sum
-    int ncand, straddle, vk;
+    float red[FMC_THREADS / 64];      // per-wave sums of exp(l - max)
+    float inv;                        // 1 / softmax sum
+    int ncand, vk, pconv;
     float s_val[64];                  // cpu_topk slots (serial replay)
     int s_id[64];
 };
@@ -827,19 +828,20 @@ FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k, const int *rsel = nullptr, 
 
 // Routing of one token in every workgroup of the one-workgroup-per-CU kernel
 // (FmDecodeArgs::route_logits): cpu_softmax / cpu_topk / cpu_normalize_weights
-// (cpu_kernels.h:263-309).  Thread t holds logit t (E <= FMC_THREADS).
+// (cpu_kernels.h:263-309).  Every wave holds all E <= FMC_THREADS logits.
 //  * softmax with the arithmetic of fm_route_kernel (same per-wave sums, added
 //    in wave order; the waves past E add zeros), so the probabilities are
 //    bit-equal to that kernel's;
-//  * the top-K SET: any element of the K largest lies at or above the K-th
-//    largest of its own 64-element chunk, so the chunk lower bounds of
-//    fm_kth_lower_bound keep ~K candidates a chunk; each candidate counts the
-//    candidates ahead of it (larger, or equal with a lower index).  Unless a
-//    run of equal probabilities straddles the K-th place, the K largest are
-//    exactly cpu_topk's slots (a strictly larger newcomer is needed to evict,
-//    and it can only evict an element with K others at or above it); with a
-//    straddling tie wavefront 0 replays cpu_topk (fm_topk_serial), which
-//    settles which of the equal elements stay.
+//  * the top-K SET, chosen on e = exp(l - max) while the sum is still being
+//    exchanged: any element of the K largest lies at or above the K-th largest
+//    of its own 64-element chunk, so the chunk lower bounds of
+//    fm_kth_lower_bound keep ~K candidates a chunk, and each candidate counts
+//    the candidates ahead of it (larger e, or equal e and a lower index).
+//    p = e * (1 / sum) is monotone in e, so unless p at the K-th place equals
+//    p at the (K+1)-th, the K first are exactly cpu_topk's slots (a strictly
+//    larger newcomer is needed to evict, and it can only evict an element with
+//    K others at or above it); with equal p across that place wavefront 0
+//    replays cpu_topk (fm_topk_serial), which settles which of them stay.
 // L.rsel / L.rp receive the set in descending order (the kernel's slot order:
 // only the order of the weighted sum differs from cpu_topk's slots, a
 // rounding-level difference); returns 1 / sum of the selected probabilities,
@@ -850,7 +852,7 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
     constexpr int NW = FMC_THREADS / 64;
     FmcRoute &R = L.rt;
     // every wave holds all E logits (lane l: elements l, 64 + l, ...): the
-    // max needs no exchange between waves; the per-wave sums do
+    // max needs no exchange between waves
     float mx = -INFINITY;
 #pragma unroll
     for (int q = 0; q < NW; q++) mx = fmaxf(mx, lgq[q]);
@@ -861,37 +863,40 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
     for (int q = 1; q < NW; q++) lg = wv == q ? lgq[q] : lg;
     const float ev = tid < E ? expf(lg - mx) : 0.f;
     const float ws = fm_lane_sum<64>(ev);
-    if (lane == 0) R.red[1][wv] = ws;
-    __syncthreads();
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) sum += R.red[1][w];
-    const float inv = 1.0f / sum;
-    const int pv = tid < E ? __float_as_int(ev * inv) : -2;
-    FM_DX_MARK(9);
-    if (tid < nch * 64) R.pb[tid] = pv;
+    if (lane == 0) R.red[wv] = ws;
+    // candidates on e = exp(l - max), before the sum is known: p = e * (1 /
+    // sum) is monotone in e, so the K largest by e are cpu_topk's set unless
+    // p rounds equal across the K-th place (checked below on p itself)
+    const int eb = tid < E ? __float_as_int(ev) : -2;
+    if (tid < nch * 64) R.pb[tid] = eb;
     if (wv < nch) {
-        const int res = fm_kth_lower_bound(pv, K);
-        const uint64_t m = __ballot(pv >= res);
+        const int res = fm_kth_lower_bound(eb, K);
+        const uint64_t m = __ballot(eb >= res);
         int base = 0;
         if (lane == 0) base = atomicAdd(&R.ncand, __builtin_popcountll(m));
         base = __builtin_amdgcn_readlane(base, 0);
         if ((m >> lane) & 1ull) {
             const int pos = base + fm_mbcnt(m);
-            R.cv[pos] = pv;
+            R.cv[pos] = eb;
             R.ci[pos] = tid;
         }
     }
     __syncthreads();
     FM_DX_MARK(10);
+    // the softmax sum with fm_route_kernel's arithmetic (the same per-wave
+    // sums added in wave order; waves past E add zeros), so p is bit-equal
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) sum += R.red[w];
+    const float inv = 1.0f / sum;
     const int NC = R.ncand;
+    // a candidate's place = the number of candidates ahead of it by the key
+    // (e bits, then the lower index first): unique places, so place K - 1 is
+    // the last selected and place K the first left out
     if (NC <= FMC_THREADS / 8) {
-        // eight lanes per candidate (lane r: entries 12 r .. 12 r + 11); a
-        // candidate's place = the number of candidates ahead of it by the key
-        // (probability bits, then the lower index first), counted on 64-bit
-        // keys, summed over the 8 lanes (quad_perm [1,0,3,2], [2,3,0,1],
-        // row_half_mirror).  Places K-1 and K then tell whether a run of
-        // equal probabilities straddles the K-th place.
+        // eight lanes per candidate (lane r: entries 12 r .. 12 r + 11), 64-bit
+        // keys, counts summed over the 8 lanes (quad_perm [1,0,3,2],
+        // [2,3,0,1], row_half_mirror)
         const int c = tid >> 3, r = tid & 7;
         const bool act = c < NC;
         const uint64_t key = act ? ((uint64_t)(uint32_t)R.cv[c] << 32) | (uint32_t)(1023 - R.ci[c]) : 0;
@@ -918,45 +923,50 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
         cnt += fm_dpp_i<0x4E>(cnt);
         cnt += fm_dpp_i<0x141>(cnt);
         if (act && r == 0) {
+            const int pbits = __float_as_int(__int_as_float((int)(key >> 32)) * inv);
             if (cnt < K) {
                 L.rsel[cnt] = (int)(1023 - (uint32_t)key);
-                L.rp[cnt] = (int)(key >> 32);
+                L.rp[cnt] = pbits;
             } else if (cnt == K) {
-                R.vk = (int)(key >> 32);  // the first probability left out
+                R.vk = pbits;
             }
         }
     } else if (tid < NC) {
         const int v = R.cv[tid], me = R.ci[tid];
-        int gt = 0, ahead = 0, eq = 0;
+        int pos = 0;
         for (int j = 0; j < NC; j += 4) {
             const int4 c = *reinterpret_cast<const int4 *>(&R.cv[j]);
             const int4 d = *reinterpret_cast<const int4 *>(&R.ci[j]);
             const int cc[4] = {c.x, c.y, c.z, c.w}, dd[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const bool in = j + q < NC;
-                gt += in && cc[q] > v;
-                eq += in && cc[q] == v;
-                ahead += in && cc[q] == v && dd[q] < me;
-            }
+            for (int q = 0; q < 4; q++) pos += j + q < NC && (cc[q] > v || (cc[q] == v && dd[q] < me));
         }
-        const int pos = gt + ahead;
+        const int pbits = __float_as_int(__int_as_float(v) * inv);
         if (pos < K) {
             L.rsel[pos] = me;
-            L.rp[pos] = v;
+            L.rp[pos] = pbits;
+        } else if (pos == K) {
+            R.vk = pbits;
         }
-        if (gt < K && gt + eq > K) R.straddle = 1;
     }
+    if (tid == 0) R.inv = inv;
     __syncthreads();
     FM_DX_MARK(11);
-    if (R.straddle || (NC <= FMC_THREADS / 8 && R.vk == L.rp[K - 1])) {  // uniform: read after the barrier
+    if (R.vk == L.rp[K - 1]) {  // uniform (read after the barrier): equal p across the K-th place
         if (wv == 0) {
+            // p for every element, then cpu_topk's replacement history decides
+            for (int i = lane; i < nch * 64; i += 64) {
+                const int v = R.pb[i];
+                R.pb[i] = v >= 0 ? __float_as_int(__int_as_float(v) * inv) : v;
+            }
+            fm_wave_lds_sync();
             fm_topk_serial(R.pb, E, K, R);
             fm_wave_lds_sync();
             if (lane < K) {
                 L.rsel[lane] = R.s_id[lane];
                 L.rp[lane] = __float_as_int(R.s_val[lane]);
             }
+            if (lane == 0) R.pconv = 1;
         }
         __syncthreads();
     }
@@ -1002,8 +1012,8 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     if (tid == 0) {
         L.xready = L.dn_ready = 0;
         if constexpr (RT) {
-            L.rt.ncand = L.rt.straddle = 0;  // fused routing: candidate count, tie flag
-            L.rt.vk = -1;                      // ... and the first probability left out (none)
+            L.rt.ncand = L.rt.pconv = 0;  // fused routing: candidate count, p written into pb
+            L.rt.vk = -1;                 // ... and the first probability left out (none)
         }
     }
     __syncthreads();
@@ -1357,6 +1367,11 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         // no item, so its CU makes no down-row copy over the routing scratch):
         // cpu_topk's slot order by serial replay, then cpu_normalize_weights
         // (sequential sum over the slots) -- bit-equal to fm_route_kernel
+        if (!L.rt.pconv) {
+            for (int i = lane; i < a.route_E; i += 64)
+                L.rt.pb[i] = __float_as_int(__int_as_float(L.rt.pb[i]) * L.rt.inv);
+            fm_wave_lds_sync();
+        }
         fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt);
         fm_wave_lds_sync();
         if (lane < a.K) {
