@@ -61,11 +61,16 @@ static int moe_forward_impl(const char *who, const fm_moe_layer *L, int K, const
     };
     int rc = fm_batch_matvec(h_post, L->pool.hidden, specs, L->has_shared ? 2 : 1, stream);
     if (rc) return rc;
-    /* softmax -> top-K -> renormalise (3519-3523) */
+    /* softmax -> top-K -> renormalise (3519-3523), then CMD3: experts + shared
+     * expert + combine (3895-3993) -- one launch where the routing fuses into
+     * the step */
+    if (!norm_w && L->pool.num_experts <= 4096)
+        return fm_moe_route_decode_pool(&L->pool, logits, (int)L->pool.num_experts, K, idx, w,
+                                        L->has_shared ? &L->shared : NULL, L->shared_bits, L->shared_inter,
+                                        L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16, p, rest, stream);
     rc = fm_route_topk(logits, 1, (int)L->pool.num_experts, K, idx, w, stream);
     if (rc) return rc;
-    /* CMD3: experts + shared expert + combine (3895-3993), optionally the next
-     * layer's input RMS norm (3995-4029) */
+    /* ... with the next layer's input RMS norm (3995-4029) */
     if (norm_w)
         return fm_moe_decode_pool_norm(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL, L->shared_bits,
                                        L->shared_inter, L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16, norm_w, eps,

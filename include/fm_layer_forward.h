@@ -36,7 +36,8 @@ size_t fm_moe_forward_workspace_size(const fm_moe_layer *L, int K);
  *   logits = router(h_post); g = seg(h_post)                  (3506-3512)
  *   idx, w = topK(softmax(logits)), renormalised               (3519-3523)
  *   out = h_mid + sum_k w_k E_idx[k](h_post) + sigmoid(g) S(h_post)
- * h_post, h_mid, out: device [hidden] fp32; out_bf16 optional. */
+ * h_post, h_mid, out: device [hidden] fp32; out_bf16 optional.  Routing and
+ * the expert step run as one launch (fm_moe_route_decode_pool). */
 int fm_moe_forward(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
                    float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
 
