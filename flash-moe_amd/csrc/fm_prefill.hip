@@ -233,6 +233,77 @@ __global__ __launch_bounds__(256) void fm_pf_xop_kernel(const float *__restrict_
     }
 }
 
+// Rows of up to 4096 inputs: each thread converts one quarter group (16
+// elements) held in registers (one load pass), TPR = in_dim / 16 threads per
+// row and 256 / TPR rows per workgroup, so short rows (the 1024 activations of
+// an entry) fill the workgroup.  Same outputs as fm_pf_xop_kernel.
+template <int TPR>
+__global__ __launch_bounds__(256) void fm_pf_xop1_kernel(const float *__restrict__ src, const float *__restrict__ src2,
+                                                         const int *__restrict__ nrows_dev, int nrows_max,
+                                                         uint32_t in_dim, fm_h2 *x4, fm_h2 *x2, fm_h2 *l4, fm_h2 *l2,
+                                                         float *xsum, float *xinv) {
+    constexpr int RPW = 256 / TPR;  // rows per workgroup
+    constexpr int WPR = TPR >= 64 ? TPR / 64 : 1;  // waves per row
+    __shared__ float wmax[4];
+    const uint32_t G = in_dim / 64;
+    const int tid = threadIdx.x;
+    const uint32_t row = blockIdx.x * RPW + tid / TPR, qi = tid % TPR;
+    const int nrows = nrows_dev ? *nrows_dev : nrows_max;
+    const bool live = row < (uint32_t)nrows;
+    const size_t rbase = (size_t)(live ? row : 0) * in_dim;
+    float v[16];
+    pf_xop_load16(src, src2, rbase + 16 * qi, v);
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+    for (int o = 1; o < (TPR < 64 ? TPR : 64); o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if constexpr (WPR > 1) {
+        if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+        __syncthreads();
+        const int w0 = (tid >> 6) & ~(WPR - 1);
+#pragma unroll
+        for (int w = 0; w < WPR; w++) mx = fmaxf(mx, wmax[w0 + w]);
+    }
+    if (!live) return;
+    const int ex = fm_group_shift(mx);
+    const float f = fm_exp2i(ex), fs = fm_exp2i(ex - 24);
+    if (qi == 0) xinv[row] = fm_exp2i(24 - ex);
+    float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
+#pragma unroll
+    for (int n = 0; n < 8; n++) mt[n] *= f;
+    const uint32_t g = qi / 4, qq = qi & 3;
+    const size_t base = ((size_t)row * G + g) * 32;
+    fm_h2 h4[8], h2[8];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float m = (j & 1) ? 0.0625f * f : f;
+            const float a = v[8 * h + j] * m, b = v[8 * h + 4 + j] * m;
+            h4[4 * h + j] = fm_pack_h2(a, b);
+            if (l4) l4[base + 4 * (2 * qq + h) + j] = fm_pack_h2(a - (float)h4[4 * h + j].x, b - (float)h4[4 * h + j].y);
+        }
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const float a = v[n] * mt[n], b = v[8 + n] * mt[n];
+        h2[n] = fm_pack_h2(a, b);
+        if (l2) l2[base + 8 * qq + n] = fm_pack_h2(a - (float)h2[n].x, b - (float)h2[n].y);
+    }
+    // this thread's eight pairs of either layout are contiguous: two 16-byte stores each
+    fm_u4 *d4 = (fm_u4 *)(x4 + base + 8 * qq), *d2 = (fm_u4 *)(x2 + base + 8 * qq);
+    d4[0] = (fm_u4){__builtin_bit_cast(uint32_t, h4[0]), __builtin_bit_cast(uint32_t, h4[1]), __builtin_bit_cast(uint32_t, h4[2]), __builtin_bit_cast(uint32_t, h4[3])};
+    d4[1] = (fm_u4){__builtin_bit_cast(uint32_t, h4[4]), __builtin_bit_cast(uint32_t, h4[5]), __builtin_bit_cast(uint32_t, h4[6]), __builtin_bit_cast(uint32_t, h4[7])};
+    d2[0] = (fm_u4){__builtin_bit_cast(uint32_t, h2[0]), __builtin_bit_cast(uint32_t, h2[1]), __builtin_bit_cast(uint32_t, h2[2]), __builtin_bit_cast(uint32_t, h2[3])};
+    d2[1] = (fm_u4){__builtin_bit_cast(uint32_t, h2[4]), __builtin_bit_cast(uint32_t, h2[5]), __builtin_bit_cast(uint32_t, h2[6]), __builtin_bit_cast(uint32_t, h2[7])};
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    if (qq == 0) xsum[(size_t)row * G + g] = sm * fs;
+}
+
 // ---------------------------------------------------------------- gemm -----
 // One block = 4 waves = 64 rows (16 per wave) of ONE matrix x one chunk of <=
 // 16 entries of one expert.  The input dimension is walked in pieces of 8
@@ -946,10 +1017,20 @@ extern "C" size_t fm_prefill_moe_workspace_size(int T, int K, const fm_expert_po
 
 static int pf_launch_ops(const float *src, const float *src2, const int *nrows_dev, int nrows_max, uint32_t in_dim,
                          char *base, const PfOps &P, bool lo, hipStream_t st) {
+    fm_h2 *x4 = (fm_h2 *)(base + P.x4), *x2 = (fm_h2 *)(base + P.x2);
+    fm_h2 *l4 = lo ? (fm_h2 *)(base + P.l4) : nullptr, *l2 = lo ? (fm_h2 *)(base + P.l2) : nullptr;
+    float *sum = (float *)(base + P.sum), *inv = (float *)(base + P.inv);
+    const uint32_t tpr = in_dim / 16;
+#define PF_XOP1(TPR)                                                                                             \
+    if (tpr == TPR) {                                                                                            \
+        hipLaunchKernelGGL(fm_pf_xop1_kernel<TPR>, dim3((unsigned)((nrows_max + 256 / TPR - 1) / (256 / TPR))), \
+                           dim3(256), 0, st, src, src2, nrows_dev, nrows_max, in_dim, x4, x2, l4, l2, sum, inv); \
+        return fm_check_launch("fm_pf_xop1_kernel");                                                             \
+    }
+    PF_XOP1(256) PF_XOP1(128) PF_XOP1(64) PF_XOP1(32) PF_XOP1(16) PF_XOP1(8) PF_XOP1(4)
+#undef PF_XOP1
     hipLaunchKernelGGL(fm_pf_xop_kernel, dim3((unsigned)nrows_max), dim3(256), 0, st, src, src2, nrows_dev,
-                       nrows_max, in_dim, (fm_h2 *)(base + P.x4), (fm_h2 *)(base + P.x2),
-                       lo ? (fm_h2 *)(base + P.l4) : nullptr, lo ? (fm_h2 *)(base + P.l2) : nullptr,
-                       (float *)(base + P.sum), (float *)(base + P.inv));
+                       nrows_max, in_dim, x4, x2, l4, l2, sum, inv);
     return fm_check_launch("fm_pf_xop_kernel");
 }
 
