@@ -792,13 +792,39 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
     __syncthreads();
     const int n = T * K;
-    for (int i = tid; i < n; i += blockDim.x) {
-        int e = idx[i];
-        if (e < 0 || e >= E) {
-            atomicOr(err, FM_STATUS_BAD_EXPERT);
-            continue;
+    // up to PF_LQ entries per thread keep their expert and their place in its
+    // list (the count's atomic result) in registers for the scatter below
+    constexpr int PF_LQ = 16;
+    const bool inreg = n <= PF_LQ * 1024;
+    int le[PF_LQ], lp[PF_LQ];
+#pragma unroll
+    for (int j = 0; j < PF_LQ; j++) {
+        const int i = tid + 1024 * j;
+        le[j] = -1;
+        lp[j] = 0;
+        if (inreg && i < n) le[j] = idx[i];
+    }
+    if (inreg) {
+#pragma unroll
+        for (int j = 0; j < PF_LQ; j++) {
+            const int e = le[j];
+            if (tid + 1024 * j >= n) continue;
+            if (e < 0 || e >= E) {
+                atomicOr(err, FM_STATUS_BAD_EXPERT);
+                le[j] = -1;
+                continue;
+            }
+            lp[j] = atomicAdd(&cnt[e], 1);
         }
-        atomicAdd(&cnt[e], 1);
+    } else {
+        for (int i = tid; i < n; i += blockDim.x) {
+            int e = idx[i];
+            if (e < 0 || e >= E) {
+                atomicOr(err, FM_STATUS_BAD_EXPERT);
+                continue;
+            }
+            atomicAdd(&cnt[e], 1);
+        }
     }
     if (has_shared && tid == 0) cnt[E] = T;
     __syncthreads();
@@ -877,18 +903,29 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             for (int ei = nn; ei < PF_CHUNK; ei++) row[16 + ei] = -1;
         }
     }
-    // scatter entries (slot id t*K + k) into the entry lists and the chunk rows;
-    // cnt becomes a running cursor
+    // scatter entries (slot id t*K + k) into the entry lists and the chunk rows
     __syncthreads();
-    for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += blockDim.x) {
-        const int e = idx[i];
-        if (e < 0 || e >= E) continue;
-        const int p = atomicAdd(&cnt[e], 1);
-        entries[base[e] + p] = i;
-        const int ci = cbase[e] + p / PF_CHUNK;
-        if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
+    if (inreg) {
+#pragma unroll
+        for (int j = 0; j < PF_LQ; j++) {
+            const int e = le[j], p = lp[j], i = tid + 1024 * j;
+            if (e < 0) continue;
+            entries[base[e] + p] = i;
+            const int ci = cbase[e] + p / PF_CHUNK;
+            if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
+        }
+    } else {
+        // cnt becomes a running cursor
+        for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += blockDim.x) {
+            const int e = idx[i];
+            if (e < 0 || e >= E) continue;
+            const int p = atomicAdd(&cnt[e], 1);
+            entries[base[e] + p] = i;
+            const int ci = cbase[e] + p / PF_CHUNK;
+            if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
+        }
     }
     if (has_shared)
         for (int t = tid; t < T; t += blockDim.x) {
