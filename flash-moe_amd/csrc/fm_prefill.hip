@@ -954,6 +954,53 @@ __global__ __launch_bounds__(256) void fm_pf_combine_kernel(const float *y, cons
     if (out_bf16) out_bf16[(size_t)t * H + i] = fm_f32_to_bf16(v);
 }
 
+// The same combine, four consecutive elements a thread (16-byte loads and
+// stores; every slot's row issued before the sums, which run in slot order as
+// above).  Needs hidden % 4 == 0 and 16-byte aligned y / h_mid / out.
+__global__ __launch_bounds__(256) void fm_pf_combine4_kernel(const float *y, const float *w, int T, int K, int H,
+                                                             int has_shared, const float *g, const float *h_mid,
+                                                             float *out, uint16_t *out_bf16) {
+    const int t = blockIdx.y;
+    const int i = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= H || t >= T) return;
+    fm_f4 yk[FM_MAX_K + 1];
+#pragma unroll
+    for (int k = 0; k < FM_MAX_K; k++)
+        if (k < K) yk[k] = fm_ldg_f4(y + (size_t)(t * K + k) * H + i);
+    if (has_shared) yk[FM_MAX_K] = fm_ldg_f4(y + (size_t)(T * K + t) * H + i);
+    float m[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < FM_MAX_K; k++) {
+        if (k < K) {
+            const float wk = w[t * K + k];
+            m[0] = __fadd_rn(m[0], __fmul_rn(wk, yk[k].x));
+            m[1] = __fadd_rn(m[1], __fmul_rn(wk, yk[k].y));
+            m[2] = __fadd_rn(m[2], __fmul_rn(wk, yk[k].z));
+            m[3] = __fadd_rn(m[3], __fmul_rn(wk, yk[k].w));
+        }
+    }
+    float v[4] = {m[0], m[1], m[2], m[3]};
+    if (h_mid) {
+        const fm_f4 hm = fm_ldg_f4(h_mid + (size_t)t * H + i);
+        v[0] = __fadd_rn(hm.x, m[0]);
+        v[1] = __fadd_rn(hm.y, m[1]);
+        v[2] = __fadd_rn(hm.z, m[2]);
+        v[3] = __fadd_rn(hm.w, m[3]);
+    }
+    if (has_shared) {
+        const float sw = g ? fm_sigmoid(g[t]) : 1.0f;
+        const float ys[4] = {yk[FM_MAX_K].x, yk[FM_MAX_K].y, yk[FM_MAX_K].z, yk[FM_MAX_K].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = __fadd_rn(v[j], __fmul_rn(sw, ys[j]));
+    }
+    *(fm_f4 *)(out + (size_t)t * H + i) = (fm_f4){v[0], v[1], v[2], v[3]};
+    if (out_bf16) {
+        const uint32_t lo = (uint32_t)fm_f32_to_bf16(v[0]) | ((uint32_t)fm_f32_to_bf16(v[1]) << 16);
+        const uint32_t hi = (uint32_t)fm_f32_to_bf16(v[2]) | ((uint32_t)fm_f32_to_bf16(v[3]) << 16);
+        *(uint2 *)(out_bf16 + (size_t)t * H + i) = make_uint2(lo, hi);
+    }
+}
+
 // SwiGLU of the apart shared expert's gate and up rows, in place into g.
 __global__ __launch_bounds__(256) void fm_pf_swiglu_kernel(float *g, const float *u, size_t n) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -1265,6 +1312,14 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
         if (rc) return rc;
     }
     // combine
+    const bool vec4 = pool->hidden % 4 == 0 && K <= FM_MAX_K && !(((uintptr_t)y | (uintptr_t)out) & 15) &&
+                      !((uintptr_t)h_mid & 15) && !((uintptr_t)out_bf16 & 7);
+    if (vec4) {
+        dim3 cg4((pool->hidden / 4 + 255) / 256, T);
+        hipLaunchKernelGGL(fm_pf_combine4_kernel, cg4, dim3(256), 0, st, y, weights, T, K, (int)pool->hidden,
+                           has_shared, shared_gate_scores, h_mid, out, out_bf16);
+        return fm_check_launch("fm_pf_combine4_kernel");
+    }
     dim3 cg((pool->hidden + 255) / 256, T);
     hipLaunchKernelGGL(fm_pf_combine_kernel, cg, dim3(256), 0, st, y, weights, T, K, (int)pool->hidden, has_shared,
                        shared_gate_scores, h_mid, out, out_bf16);
