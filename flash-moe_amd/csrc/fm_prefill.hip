@@ -65,7 +65,6 @@ struct PfArgs {
     // work lists
     const int *chunks;  // [max_chunks][PF_CROW] chunk rows (see fm_pf_lists_kernel)
     const int *nchunks;
-    const int *entries;  // entry -> slot id
     int T, K;
     uint32_t max_chunks;
     uint32_t xcd_slots;  // workgroups one XCD runs at once (eight-stage kernel: its CUs)
@@ -335,6 +334,9 @@ __global__ __launch_bounds__(256) void fm_pf_xop1_kernel(const float *__restrict
 #define PF_KS(W) (PF_TOK * PF_GPP * 8 / (64 * (W)))
 #ifndef FM_PF_MARK
 #define FM_PF_MARK(n)
+#endif
+#ifndef FM_PL_MARK
+#define FM_PL_MARK(n)
 #endif
 
 template <bool LO>
@@ -729,7 +731,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO || !RES ? 2 : PF_MINB)) 
     const char *blob = (const char *)(((uint64_t)(uint32_t)ch[5] << 32) | (uint32_t)ch[4]);
     if (threadIdx.x < PF_TOK) {
         const int ei = threadIdx.x;
-        const int sl = ch[16 + ei];
+        const int sl = ei < n ? ch[16 + ei] : -1;  // ids past the count are not written
         const int sr = sl < 0 ? -1 : (a.mode == 1 ? off + ei : (a.mode == 2 ? sl : pf_token_of_slot(a, sl)));
         slot_s[ei] = sl;
         srow_s[ei] = sr;
@@ -780,17 +782,33 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO || !RES ? 2 : PF_MINB)) 
 // needs in ONE dependent load.
 __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T, int K, int E, int has_shared,
                                                            const void *const *blobs, const uint8_t *bits_table,
-                                                           int sh_bits, int *entries, int *chunks, int *nchunks,
+                                                           int sh_bits, int *chunks, int *nchunks,
                                                            uint32_t max_chunks, int *err) {
     extern __shared__ int sm[];
     int *cnt = sm;               // [E + 1]
     int *base = sm + (E + 1);    // [E + 2]
     int *cbase = base + (E + 2); // [E + 2]
+    int *tbits = cbase + (E + 2);  // [E + 1] bit widths
+    uint64_t *tblob = (uint64_t *)(((uintptr_t)(tbits + E + 1) + 7) & ~(uintptr_t)7);  // [E] blob addresses
     __shared__ int wsum[2][16];
+    FM_PL_MARK(0);
     const int NE = E + (has_shared ? 1 : 0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // the pool table entries the chunk rows need (E <= 4096), loaded now (they
+    // arrive while the entries are counted) and staged in LDS before the scan
+    constexpr int PF_LT = 4;  // entries per thread
+    const bool tstage = E <= PF_LT * 1024;
+    uint64_t pbl[PF_LT];
+    int pbt[PF_LT];
+#pragma unroll
+    for (int j = 0; j < PF_LT; j++) {
+        const int e = tid + 1024 * j;
+        pbl[j] = tstage && e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
+        pbt[j] = tstage && e < E ? (int)bits_table[e] : 0;
+    }
     for (int i = tid; i <= E; i += blockDim.x) cnt[i] = 0;
     __syncthreads();
+    FM_PL_MARK(1);
     const int n = T * K;
     // up to PF_LQ entries per thread keep their expert and their place in its
     // list (the count's atomic result) in registers for the scatter below
@@ -828,6 +846,15 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     }
     if (has_shared && tid == 0) cnt[E] = T;
     __syncthreads();
+    FM_PL_MARK(2);
+#pragma unroll
+    for (int j = 0; j < PF_LT; j++) {
+        const int e = tid + 1024 * j;
+        if (tstage && e < E) {
+            tblob[e] = pbl[j];
+            tbits[e] = pbt[j];
+        }
+    }
     // exclusive scans of entries and chunks over experts: thread t owns the
     // run of PER consecutive experts starting at t * PER
     {
@@ -854,6 +881,7 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             wsum[1][wv] = ic;
         }
         __syncthreads();
+    FM_PL_MARK(3);
         int pe = 0, pc = 0;
         for (int w = 0; w < wv; w++) {
             pe += wsum[0][w];
@@ -877,8 +905,10 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
         }
     }
     __syncthreads();
-    // chunk rows: header and empty slot ids (the scatter fills the live ones),
-    // one thread per chunk; its expert is the last e with cbase[e] <= chunk
+    FM_PL_MARK(4);
+    // chunk rows: the header (the scatter fills the live slot ids; the GEMMs
+    // read none past the count), one thread per chunk; its expert is the last
+    // e with cbase[e] <= chunk
     {
         const int nc = min(cbase[NE], (int)max_chunks);
         for (int ci = tid; ci < nc; ci += blockDim.x) {
@@ -891,26 +921,25 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
                     hi = mid;
             }
             const int e = lo, j = ci - cbase[e], ne = cnt[e];
-            const uint64_t blob = e < E ? (uint64_t)(uintptr_t)blobs[e] : 0ull;
+            const uint64_t blob = e < E ? (tstage ? tblob[e] : (uint64_t)(uintptr_t)blobs[e]) : 0ull;
             int *row = chunks + (size_t)PF_CROW * ci;
             const int nn = min(PF_CHUNK, ne - j * PF_CHUNK);
             row[0] = e;
             row[1] = base[e] + j * PF_CHUNK;
             row[2] = nn;
-            row[3] = e < E ? (int)bits_table[e] : sh_bits;
+            row[3] = e < E ? (tstage ? tbits[e] : (int)bits_table[e]) : sh_bits;
             row[4] = (int)(uint32_t)blob;
             row[5] = (int)(uint32_t)(blob >> 32);
-            for (int ei = nn; ei < PF_CHUNK; ei++) row[16 + ei] = -1;
         }
     }
-    // scatter entries (slot id t*K + k) into the entry lists and the chunk rows
+    // scatter the entries (slot id t*K + k) into the chunk rows
     __syncthreads();
+    FM_PL_MARK(5);
     if (inreg) {
 #pragma unroll
         for (int j = 0; j < PF_LQ; j++) {
             const int e = le[j], p = lp[j], i = tid + 1024 * j;
             if (e < 0) continue;
-            entries[base[e] + p] = i;
             const int ci = cbase[e] + p / PF_CHUNK;
             if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
         }
@@ -922,17 +951,16 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
             const int e = idx[i];
             if (e < 0 || e >= E) continue;
             const int p = atomicAdd(&cnt[e], 1);
-            entries[base[e] + p] = i;
             const int ci = cbase[e] + p / PF_CHUNK;
             if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + p % PF_CHUNK] = i;
         }
     }
     if (has_shared)
         for (int t = tid; t < T; t += blockDim.x) {
-            entries[base[E] + t] = T * K + t;
             const int ci = cbase[E] + t / PF_CHUNK;
             if (ci < (int)max_chunks) chunks[(size_t)PF_CROW * ci + 16 + t % PF_CHUNK] = T * K + t;
         }
+    FM_PL_MARK(9);
 }
 
 // ---------------------------------------------------------------- combine --
@@ -1042,7 +1070,7 @@ static PfOps pf_ops_layout(size_t rows, uint32_t in_dim, bool lo, size_t o) {
 }
 
 struct PfLayout {
-    size_t entries, chunks, nchunks, err, gout, uout, y, total;
+    size_t chunks, nchunks, err, gout, uout, y, total;
     PfOps xo, ao;
     size_t sh_ws, sh_ws_bytes, sh_g, sh_u;  // shared expert of its own intermediate size (sh_ws_bytes > 0)
 };
@@ -1064,8 +1092,6 @@ static PfLayout pf_layout(int T, int K, uint32_t E, uint32_t hidden, uint32_t in
     // the decode kernels' tagged region for the few-token paths (T <= 8): kept
     // apart from the GEMM arrays below, so it only ever holds tagged words
     o = fm_moe_decode_workspace_size(FM_PREFILL_DECODE_MAX_T * (FM_MAX_K + 1), hidden, inter);
-    L.entries = o;
-    o += fm_align_up(nent * 4, 256);
     L.chunks = o;
     o += fm_align_up((size_t)mc * PF_CROW * 4, 256);
     L.nchunks = o;
@@ -1233,9 +1259,10 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
 
     // lists
     size_t lds = ((size_t)pool->num_experts * 3 + 5) * sizeof(int);
+    if (pool->num_experts <= 4096) lds += ((size_t)pool->num_experts + 1) * sizeof(int) + 8 + (size_t)pool->num_experts * 8;
     if (lds > 65536) return fm_fail(FM_ERR_UNSUPPORTED, "%s: too many experts", who);
     hipLaunchKernelGGL(fm_pf_lists_kernel, dim3(1), dim3(1024), lds, st, idx, T, K, (int)pool->num_experts,
-                       grouped_shared, pool->blobs, pool->bits, shared ? shared_bits : 4, (int *)(p + L.entries),
+                       grouped_shared, pool->blobs, pool->bits, shared ? shared_bits : 4,
                        (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err));
     int rc = fm_check_launch("fm_pf_lists_kernel");
     if (rc) return rc;
@@ -1266,7 +1293,6 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     a.E = (int)pool->num_experts;
     a.chunks = (const int *)(p + L.chunks);
     a.nchunks = (const int *)(p + L.nchunks);
-    a.entries = (const int *)(p + L.entries);
     a.T = T;
     a.K = K;
     a.max_chunks = mc;
@@ -1329,9 +1355,8 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
 // ---------------------------------------------------------------- pfb gemm -
 // Y[N, out] = X[N, in] dequant(W)^T, X fp32 (fp16 hi + lo terms), one
 // "expert" whose entry list is the identity.
-__global__ void fm_pfb_lists_kernel(int N, int *entries, int *chunks, int *nchunks) {
+__global__ void fm_pfb_lists_kernel(int N, int *chunks, int *nchunks) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < N) entries[i] = i;
     const int nc = (N + PF_CHUNK - 1) / PF_CHUNK;
     if (i < nc) {
         int *row = chunks + (size_t)PF_CROW * i;
@@ -1347,10 +1372,10 @@ __global__ void fm_pfb_lists_kernel(int N, int *entries, int *chunks, int *nchun
 }
 
 // [256 B left alone: the status word of a layer workspace that shares this
-// region][entries][chunk rows][nchunks], then the operands
+// region][chunk rows][nchunks], then the operands
 static size_t pfb_head(uint32_t N) {
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    return 256 + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256) + 256;
+    return 256 + fm_align_up(nc * PF_CROW * 4, 256) + 256;
 }
 
 extern "C" size_t fm_pfb_gemm_workspace_size(uint32_t N, uint32_t in_dim) {
@@ -1371,13 +1396,12 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     if ((uintptr_t)X & 15) return fm_fail(FM_ERR_INVALID, "%s: X not 16-byte aligned", who);
     if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     char *p = (char *)ws;
-    int *entries = (int *)(p + 256);
-    int *chunks = (int *)(p + 256 + fm_align_up((size_t)N * 4, 256));
+    int *chunks = (int *)(p + 256);
     const size_t nc = (N + PF_CHUNK - 1) / PF_CHUNK;
-    int *nchunks = (int *)(p + 256 + fm_align_up((size_t)N * 4, 256) + fm_align_up(nc * PF_CROW * 4, 256));
+    int *nchunks = (int *)(p + 256 + fm_align_up(nc * PF_CROW * 4, 256));
     hipStream_t st = fm_stream(stream);
-    const uint32_t nt = (uint32_t)(N > nc ? N : nc);
-    hipLaunchKernelGGL(fm_pfb_lists_kernel, dim3((nt + 255) / 256), dim3(256), 0, st, (int)N, entries, chunks, nchunks);
+    hipLaunchKernelGGL(fm_pfb_lists_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, (int)N, chunks,
+                       nchunks);
     rc = fm_check_launch("fm_pfb_lists_kernel");
     if (rc) return rc;
     const PfOps P = pf_ops_layout(N, in_dim, true, pfb_head(N));
@@ -1391,7 +1415,6 @@ extern "C" int fm_pfb_gemm(const void *W, const void *scales, const void *biases
     a.pbits = bits;
     a.chunks = chunks;
     a.nchunks = nchunks;
-    a.entries = entries;
     a.T = (int)N;
     a.K = 1;
     a.max_chunks = (uint32_t)nc;
