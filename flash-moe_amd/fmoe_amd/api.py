@@ -43,6 +43,10 @@ def experts_from_blob(blob, bits, hidden, inter, group_size=64, offset=0):
     e = ExpertWeights()
     check(lib().fm_expert_from_blob(ctypes.c_void_p(blob.data_ptr() + offset), ctypes.byref(L),
                                     ctypes.byref(e)))
+    # the struct holds raw device addresses: keep the tensor alive with it (a
+    # freed block can be returned to the driver, e.g. by torch.cuda.empty_cache
+    # at the start of a graph capture, and a later launch would then fault)
+    e._blob = blob
     return e
 
 

@@ -78,7 +78,8 @@ def _check(orc, dev, hidden, inter, E, K, kind, shared=True, shared_inter=0, see
     g = np.array([rng.normal()], np.float32)
     si = shared_inter or inter
     sh_blob = synth.expert_blob((7200, K, si), hidden, si, 4) if shared else None
-    sh = fm.experts_from_blob(T(sh_blob, dev), 4, hidden, si) if shared else None
+    dsh = T(sh_blob, dev) if shared else None
+    sh = fm.experts_from_blob(dsh, 4, hidden, si) if shared else None
     ws_bytes = fm.decode_workspace_bytes_ex(K, 1 if shared else 0, hidden, inter, shared_inter)
     ws = fm.workspace(ws_bytes, dev)
     ws2 = fm.workspace(ws_bytes, dev)
