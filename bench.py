@@ -73,10 +73,13 @@ def graph_of(step, items):
     return g
 
 
-def time_graph(g, n):
-    """ms per step of a graph of n steps, HIP events around one replay."""
+def time_graph(g, n, warm=3):
+    """ms per step of a graph of n steps, HIP events around one replay, after
+    `warm` untimed replays (the first uploads the graph; the GPU's clocks settle
+    over the next few milliseconds of sustained load)."""
     import torch
-    g.replay()  # first replay uploads the graph
+    for _ in range(max(1, warm)):
+        g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -652,8 +655,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work (5 configs)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--prefill-steps", type=int, default=10)
-    ap.add_argument("--prefill-warmup", type=int, default=2)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--prefill-warmup", type=int, default=30,
+                    help="untimed layers first: the GPU's clocks take ~20 ms of sustained load to settle")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-tiered", action="store_true")
     ap.add_argument("--no-staging", action="store_true")
@@ -709,7 +713,8 @@ def main():
                                "4096->1024->4096 SwiGLU, 4-bit g64, device routing",
                    "experts_per_step": K + 1, "bytes_per_step": dec["step_bytes"],
                    "path": "fm_moe_route_decode_pool (routing fused into the step: one launch per step)",
-                   "timing": "the K timed steps recorded into one HIP graph, replayed once between HIP events",
+                   "timing": "the K timed steps recorded into one HIP graph, replayed once between HIP events "
+                             "after three untimed replays of it",
                    "two_launch_us_per_step": round(dec["two_launch_step_ms"] * 1e3, 2),
                    "eager_us_per_step": dec["eager_us_per_step"]},
         "roofline": dec["roofline"],
