@@ -975,6 +975,9 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
     return s > 0.f ? 1.0f / s : 1.0f;
 }
 
+// Slot of item position q when the combining slot S - 1 sits at position cs.
+FM_DEV int fmc_slot_at(int q, int S, int cs) { return q == cs ? S - 1 : (q == S - 1 ? cs : q); }
+
 // Barrier of the 4 waves of one item: an LDS counter that only grows (target
 // += 4 per use).  Waits on LDS operations only -- the item's weight loads stay
 // in flight across it.
@@ -1003,7 +1006,17 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     static_assert(H <= FMM_H && I <= FMM_MAXI, "LDS is sized for hidden 4096 / inter 1024");
     const uint32_t item = blockIdx.x + gridDim.x * (uint32_t)grp;
     const bool has = item < (uint32_t)a.S * TILES;
-    const int k = has ? (int)(item / TILES) : 0;  // the item's slot
+    // Item positions q = item / TILES hold slot q, except that the combining
+    // slot S - 1 trades places with position S - grid / TILES: with m =
+    // (S TILES - 1) / grid, the workgroups from S TILES - m grid on hold m
+    // items (the others m + 1), and that position is their item m - 1.  They
+    // finish their own streams first, so the combine there waits only for the
+    // other slots' outputs (measured with m = 2: 1 us off the config-2 step;
+    // with m = 1, where that item is the CU's first, 0.5 us slower: kept off)
+    const uint32_t STI = (uint32_t)a.S * TILES, G = gridDim.x, m = (STI - 1) / G;
+    const int cs = (a.mode == 0 && m >= 2 && G % TILES == 0 && STI + TILES <= (m + 1) * G) ? a.S - (int)(G / TILES)
+                                                                                          : a.S - 1;
+    const int k = has ? fmc_slot_at((int)(item / TILES), a.S, cs) : 0;  // the item's slot
     const uint32_t tile = item % TILES;
 
     FM_DX_MARK(0);
@@ -1041,7 +1054,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // stream instead of behind the last item's own activation wait.
     const uint32_t item_l = blockIdx.x + gridDim.x * (uint32_t)(FMC_NG - 1);
     const bool has_l = item_l < (uint32_t)a.S * TILES;
-    const int k_l = has_l ? (int)(item_l / TILES) : 0;
+    const int k_l = has_l ? fmc_slot_at((int)(item_l / TILES), a.S, cs) : 0;
     const FmSlot s_l = (FMC_DN_LDS && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv) : s;
     const bool dn_lds = FMC_DN_LDS && (grp == 0 ? has_l && s_l.valid : (grp == FMC_NG - 1 && doA));
     // Every gate/up load of the item.  Loads issue in order and block while
