@@ -1448,6 +1448,8 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
     const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
     const bool mine = wv < a.S;
+    // one slot: the four waves share the activation polls and operand rows
+    const bool solo = a.S == 1;
     FM_DX_MARK(0);
     const uint32_t ep_ld = fm_epoch_load(a);
     // x of the quarter: 1024 elements, 4 threads per group
@@ -1553,7 +1555,45 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     }
     FM_DX_MARK(3);
     // ---- B: the slot's 1024 activations, then 16 down rows ----
-    if (doA) {
+    if (solo && s.valid) {
+        // wave w polls activations 256 w .. 256 w + 255
+        const uint64_t *src = a.act2 + 256 * wv;
+        uint64_t t[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) t[j] = fm_get_tagged(src + 64 * j + lane);
+        uint32_t it = 0;
+        do {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < 4; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+            if (__all(ready)) break;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(src + 64 * j + lane);
+        } while (++it < FM_SPIN_MAX);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+        FM_DX_MARK(4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) L.act[0][256 * wv + 64 * j + lane] = __uint_as_float((uint32_t)t[j]);
+        __syncthreads();
+        // per group (16 threads x 4 elements): sum, operand scale 2^e, operand rows
+        const int sb = s.bits, lay = sb == 4 ? 0 : 1;
+        const uint32_t gg = tid >> 4;
+        const float *ag = &L.act[0][64 * gg + 4 * (tid & 15)];
+        float sm = (ag[0] + ag[1]) + (ag[2] + ag[3]);
+        float mx = fmaxf(fmaxf(fabsf(ag[0]), fabsf(ag[1])), fmaxf(fabsf(ag[2]), fabsf(ag[3])));
+        sm = fmm_row_sum(sm);
+        mx = fm_row16_max(mx);
+        const int ex = fm_group_shift(mx);
+        const float f = fm_exp2i(ex);
+        if ((tid & 15) == 0) {
+            L.asum[0][gg] = sm;
+            L.ainv[0][gg] = fm_exp2i(24 - ex);
+        }
+        fmm_build_pair(&L.act[0][64 * gg], sb, 2 * (tid & 15), f, &L.aq[0][lay][gg][0]);
+        fmm_build_pair(&L.act[0][64 * gg], sb, 2 * (tid & 15) + 1, f, &L.aq[0][lay][gg][0]);
+        __syncthreads();
+    } else if (!solo && doA) {
         const uint64_t *src = a.act2 + (size_t)wv * I;
         uint64_t t[16];
 #pragma unroll
@@ -1598,6 +1638,8 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
         for (int e = 0; e < 8; e++) fmm_build_pair(&L.act[wv][64 * gg], bits, 8 * qq + e, f, &L.aq[wv][lay][gg][0]);
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
+    }
+    if (doA) {
         FM_DX_MARK(5);
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         if (bits == 4)

@@ -140,6 +140,37 @@ def test_moe_decode_valid_mask_and_no_shared(orc, dev):
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("bits", [4, 2])
+def test_moe_decode_single_expert(orc, dev, bits):
+    """Config 1: one expert x router weight, no shared expert (one slot: the
+    few-slot kernel's single-slot path, where every workgroup adds the gate/up
+    partials of all tiles itself).  Three calls on one workspace, new inputs
+    each time, plus the per-expert output mode (encode_experts_batched)."""
+    import torch
+    say("moe_decode single expert", bits)
+    ws = fm.workspace(fm.decode_workspace_bytes(1, HIDDEN, INTER), dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    ob = torch.empty(HIDDEN, dtype=torch.int16, device=dev)
+    for rep in range(3):
+        blobs, x, hm, w, _ = _decode_inputs(300 + 10 * bits + rep, 1, [bits, bits])
+        ex = fm.experts_from_blob(T(blobs[0], dev), bits, HIDDEN, INTER)
+        hmd = T(hm, dev) if rep != 1 else None
+        fm.moe_decode([ex], [bits], np.array([0.37], np.float32), T(x, dev), out, ws, HIDDEN, INTER, h_mid=hmd,
+                      out_bf16=ob)
+        torch.cuda.synchronize()
+        ref = orc.moe_decode(blobs[:1], [bits], np.array([0.37], np.float32), x, HIDDEN, INTER,
+                             h_mid=hm if rep != 1 else None)
+        base = hm if rep != 1 else 0.0
+        assert norm_err(out.cpu().numpy() - base, ref - base) <= TOL_F32, rep
+        assert norm_err(bf16_out(ob.cpu().numpy()), ref) <= TOL_BF16, rep
+    assert fm.workspace_status(ws) == 0
+    eo = torch.zeros((1, HIDDEN), dtype=torch.float32, device=dev)
+    fm.encode_experts_batched([ex], [bits], T(x, dev), eo, ws, HIDDEN, INTER)
+    torch.cuda.synchronize()
+    r = orc.expert_forward(blobs[0], bits, HIDDEN, INTER, x)
+    assert norm_err(eo.cpu().numpy()[0], r) <= TOL_F32
+
+
 def test_encode_experts_batched_and_combine(orc, dev):
     import torch
     say("encode_experts_batched + combine")
