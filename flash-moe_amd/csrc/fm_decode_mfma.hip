@@ -1436,6 +1436,7 @@ struct __attribute__((aligned(16))) FmsLds {
     float asum[FMS_MAXS][FMM_GI], ainv[FMS_MAXS][FMM_GI];
     float act[FMS_MAXS][FMM_MAXI];
     float y[FMS_MAXS][16];
+    float pu[16];                 // one slot: the up wave's folded partials
     uint32_t tr[4][16 * FMM_TS];
 };
 
@@ -1448,7 +1449,8 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
     const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
     const bool mine = wv < a.S;
-    // one slot: the four waves share the activation polls and operand rows
+    // one slot: wave 0 takes the gate rows, wave 1 the up rows, wave 2 the
+    // down rows, and the four waves share the activation polls and operand rows
     const bool solo = a.S == 1;
     FM_DX_MARK(0);
     const uint32_t ep_ld = fm_epoch_load(a);
@@ -1458,15 +1460,18 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 1024 * quarter + 16 * lane + 4 * j);  // every wave: same lines
     const FmSlot s = fmc_slot(a, mine ? wv : 0);
     const bool doA = mine && s.valid;
-    const int bits = doA ? s.bits : 4;
+    const int bits = s.valid ? s.bits : 4;
+    const bool doG = solo ? s.valid && wv == 0 : doA, doU = solo ? s.valid && wv == 1 : doA;
+    const bool doD = solo ? s.valid && wv == 2 : doA;
+    const int ys = solo ? 0 : wv;  // the slot of this wave's down rows
     FmmCodes cg, cu, cdn;
     fmm_u2 sg, bg, su, bu, sdn, bdn;
-    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * quarter, doA, cg, lane, a.x);
-    fmm_issue_sb(s.gs, s.gb, rowA0, H, 16 * quarter, doA, sg, bg, lane, a.x);
-    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * quarter, doA, cu, lane, a.x);
-    fmm_issue_sb(s.us, s.ub, rowA0, H, 16 * quarter, doA, su, bu, lane, a.x);
-    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doA, cdn, lane, a.x);
-    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doA, sdn, bdn, lane, a.x);
+    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * quarter, doG, cg, lane, a.x);
+    fmm_issue_sb(s.gs, s.gb, rowA0, H, 16 * quarter, doG, sg, bg, lane, a.x);
+    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * quarter, doU, cu, lane, a.x);
+    fmm_issue_sb(s.us, s.ub, rowA0, H, 16 * quarter, doU, su, bu, lane, a.x);
+    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doD, cdn, lane, a.x);
+    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doD, sdn, bdn, lane, a.x);
     if (tid < 64) {  // wave 0 builds the quarter's 16 operand groups
         const int gg = tid >> 2, qq = tid & 3;
         float v[16];
@@ -1511,19 +1516,27 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const uint32_t ep = fm_epoch_tag(ep_ld);
     // ---- A: this quarter's partial gate/up sums of the 16 rows ----
     uint64_t *part = a.p2 + ((size_t)wv * (H / 64) + tile) * 4 * 32;  // [slot][tile][quarter][16 rows][g, u]
-    if (doA) {
+    float pg = 0.f, pu = 0.f;
+    if (doG || doU) {
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][0][0];
         if (bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            if (doG) fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            if (doU) fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         } else {
-            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            if (doG) fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            if (doU) fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         }
         FM_DX_MARK(2);
-        float pg = fmm_q_sum(fmm_fold(g0 + g1, sg, bg, &L.xsum[4 * q], &L.xinv[4 * q]));
-        float pu = fmm_q_sum(fmm_fold(u0 + u1, su, bu, &L.xsum[4 * q], &L.xinv[4 * q]));
+        if (doG) pg = fmm_q_sum(fmm_fold(g0 + g1, sg, bg, &L.xsum[4 * q], &L.xinv[4 * q]));
+        if (doU) pu = fmm_q_sum(fmm_fold(u0 + u1, su, bu, &L.xsum[4 * q], &L.xinv[4 * q]));
+        if (solo && doU && lane < 16) L.pu[lane] = pu;
+    }
+    if (solo && s.valid) {
+        __syncthreads();  // the up wave's partials
+        if (doG) pu = L.pu[lane & 15];
+    }
+    if (doG) {
         // lanes 0..15: gate of row n, lanes 16..31: up of row n - 16 (the
         // shuffle runs in the full wave: an inactive source lane reads as 0)
         const float pu_n = __shfl(pu, (lane - 16) & 63, 64);
@@ -1639,19 +1652,19 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     }
-    if (doA) {
+    if (doD) {
         FM_DX_MARK(5);
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         if (bits == 4)
-            fmm_mma<4>(cdn, &L.aq[wv][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma<4>(cdn, &L.aq[ys][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
         else
-            fmm_mma<2>(cdn, &L.aq[wv][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
-        const float y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[wv][4 * q], &L.ainv[wv][4 * q]));
+            fmm_mma<2>(cdn, &L.aq[ys][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
+        const float y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[ys][4 * q], &L.ainv[ys][4 * q]));
         if (lane < 16) {
             if (a.mode == 1)
-                a.expert_out[(size_t)wv * H + rowB0 + n] = y;
+                a.expert_out[(size_t)ys * H + rowB0 + n] = y;
             else
-                L.y[wv][n] = y;
+                L.y[ys][n] = y;
         }
     }
     FM_DX_MARK(6);
