@@ -1012,9 +1012,11 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // items (the others m + 1), and that position is their item m - 1.  They
     // finish their own streams first, so the combine there waits only for the
     // other slots' outputs (measured with m = 2: 1 us off the config-2 step;
-    // with m = 1, where that item is the CU's first, 0.5 us slower: kept off)
+    // with m = 1, where that item is the CU's first, 0.5 us slower: kept off;
+    // compiled for the 16-group instance only, the 8-group one lost 0.45 us
+    // to the extra code even with the placement off)
     const uint32_t STI = (uint32_t)a.S * TILES, G = gridDim.x, m = (STI - 1) / G;
-    const int cs = (a.mode == 0 && m >= 2 && G % TILES == 0 && STI + TILES <= (m + 1) * G) ? a.S - (int)(G / TILES)
+    const int cs = (NG == 16 && a.mode == 0 && m >= 2 && G % TILES == 0 && STI + TILES <= (m + 1) * G) ? a.S - (int)(G / TILES)
                                                                                           : a.S - 1;
     const int k = has ? fmc_slot_at((int)(item / TILES), a.S, cs) : 0;  // the item's slot
     const uint32_t tile = item % TILES;
