@@ -437,6 +437,12 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     __syncthreads();
     const uint32_t ep = fm_epoch_tag(ep_ld);
 
+    // gate/up codes of the current item: the multi-pass instance loads the
+    // next item's during the current item's down phase (the registers are
+    // free once the activations are published), so the activation wait and
+    // the down rows of one pass overlap the gate/up latency of the next
+    FmmCodes cg, cu;
+    fmm_u2 sg = {0, 0}, bg = {0, 0}, su = {0, 0}, bu = {0, 0};
     for (uint32_t b = b0; b < nitems; b += gridDim.x) {
     // The arguments are re-read from the kernarg segment per item (scalar
     // loads): hoisted out of the loop they would all stay live in registers.
@@ -448,7 +454,6 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     const int lane = tid & 63, wv = tid >> 6, n = lane & 15, q = lane >> 4;
     const int spt = a.spt;
     const uint32_t H = a.hidden, I = a.inter, GI = I / 64, tilesA = I / 16, tilesB = H / 64;
-    if (b != b0) load_x(b);
     const bool hasA = b < (uint32_t)a.S * tilesA;
     const bool hasB = b < (uint32_t)a.S * tilesB;
     const int kA = hasA ? (int)(b / tilesA) : 0;
@@ -458,12 +463,14 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     FmSlot sB;
     if constexpr (!MP) sB = L.sd[kB];
     const bool doA = hasA && sA.valid;
-    // ---- issue every weight load of this wave ----
+    // ---- this item's gate/up loads (multi-pass: issued during the previous item) ----
     const uint32_t rowA0 = (b % tilesA) * 16;
-    FmmCodes cg, cu, cdn;
-    fmm_u2 sg = {0, 0}, bg = {0, 0}, su = {0, 0}, bu = {0, 0}, sdn = {0, 0}, bdn = {0, 0};
-    fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg, lane);
-    fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu, lane);
+    FmmCodes cdn;
+    fmm_u2 sdn = {0, 0}, bdn = {0, 0};
+    if (!MP || b == b0) {
+        fmm_issue(sA.gw, sA.gs, sA.gb, sA.bits, rowA0, H, 16 * wv, doA, cg, sg, bg, lane);
+        fmm_issue(sA.uw, sA.us, sA.ub, sA.bits, rowA0, H, 16 * wv, doA, cu, su, bu, lane);
+    }
     const uint32_t rowB0 = (b % tilesB) * 64 + 16 * wv;
 
     FM_DX_MARK(1);
@@ -547,6 +554,20 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
     if constexpr (MP) sB = fmm_uniform(L.sd[kB]);  // read only now: fewer registers live during A
     const bool doB = hasB && sB.valid;
     fmm_issue(sB.dw, sB.ds, sB.db, sB.bits, rowB0, I, 0, doB, cdn, sdn, bdn, lane);
+    if constexpr (MP) {
+        // the next item's x and gate/up rows, behind this item's down rows
+        const uint32_t bn = b + gridDim.x;
+        if (bn < nitems) {
+            load_x(bn);
+            const bool hasAn = bn < (uint32_t)a.S * tilesA;
+            const int kAn = hasAn ? (int)(bn / tilesA) : 0;
+            const FmSlot sAn = fmm_uniform(L.sd[kAn]);
+            const bool doAn = hasAn && sAn.valid;
+            const uint32_t rowAn = (bn % tilesA) * 16;
+            fmm_issue(sAn.gw, sAn.gs, sAn.gb, sAn.bits, rowAn, H, 16 * wv, doAn, cg, sg, bg, lane);
+            fmm_issue(sAn.uw, sAn.us, sAn.ub, sAn.bits, rowAn, H, 16 * wv, doAn, cu, su, bu, lane);
+        }
+    }
     // ---- B: stage the slot's activations, then 16 down rows per wave ----
     if (doB) {
         constexpr int MAXQ = FMM_MAXI / 256;

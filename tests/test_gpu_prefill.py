@@ -82,6 +82,19 @@ def test_prefill_moe_vs_oracle(orc, dev, E, Tn, K, H, I, mode):
     assert norm_err(bf16_out(r["ob"]), ref) <= TOL_BF16
 
 
+@pytest.mark.parametrize("Tn,K", [(2, 10), (8, 16), (5, 7)])
+def test_prefill_few_tokens_multi_pass(orc, dev, Tn, K):
+    """2-8 tokens at the 4096 / 1024 shape: every token's slots in one
+    multi-pass decode launch (8 x (16 + shared) = 136 slots: 17 passes of the
+    512-workgroup grid, each pass loading the next one's gate/up rows)."""
+    say("prefill few tokens", Tn, K)
+    r = _prefill_case(orc, dev, 64, Tn, K, HIDDEN, INTER, lambda e: 4 if e % 4 == 0 else 2, seed=90 + Tn)
+    ref = orc.prefill_moe(r["idx"], r["w"], r["blobs"], r["bits"], r["X"], HIDDEN, INTER,
+                          shared_blob=r["shared_blob"], shared_bits=4, shared_scores=r["g"], h_mid=r["hm"])
+    assert norm_err(r["out"] - r["hm"], ref - r["hm"]) <= TOL_F32
+    assert norm_err(bf16_out(r["ob"]), ref) <= TOL_BF16
+
+
 def test_prefill_config3_vs_decode(orc, dev):
     """Full config 3: 512 tokens, 512 experts, top-10 Zipf(1.1) routing + shared.
     Sampled tokens' prefill output must match the oracle (the reference's
