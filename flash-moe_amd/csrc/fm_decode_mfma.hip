@@ -1475,8 +1475,9 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
     const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
     const bool mine = wv < a.S;
-    // one slot: wave 0 takes the gate rows, wave 1 the up rows, wave 2 the
-    // down rows, and the four waves share the activation polls and operand rows
+    // one slot: wave 0 takes the gate rows, wave 1 the up rows, waves 2 and 3
+    // half of the down rows' inputs each, and the four waves share the
+    // activation polls and operand rows
     const bool solo = a.S == 1;
     FM_DX_MARK(0);
     const uint32_t ep_ld = fm_epoch_load(a);
@@ -1488,7 +1489,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const bool doA = mine && s.valid;
     const int bits = s.valid ? s.bits : 4;
     const bool doG = solo ? s.valid && wv == 0 : doA, doU = solo ? s.valid && wv == 1 : doA;
-    const bool doD = solo ? s.valid && wv == 2 : doA;
+    const bool doD = solo ? s.valid && wv >= 2 : doA;  // one slot: waves 2, 3 take down groups 0-7, 8-15
     const int ys = solo ? 0 : wv;  // the slot of this wave's down rows
     FmmCodes cg, cu, cdn;
     fmm_u2 sg, bg, su, bu, sdn, bdn;
@@ -1496,8 +1497,13 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     fmm_issue_sb(s.gs, s.gb, rowA0, H, 16 * quarter, doG, sg, bg, lane, a.x);
     fmm_issue_codes(s.uw, bits, rowA0, H, 16 * quarter, doU, cu, lane, a.x);
     fmm_issue_sb(s.us, s.ub, rowA0, H, 16 * quarter, doU, su, bu, lane, a.x);
-    fmm_issue_codes(s.dw, bits, rowB0, I, 0, doD, cdn, lane, a.x);
-    fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doD, sdn, bdn, lane, a.x);
+    if (solo) {
+        fmm_issue_codes<8>(s.dw, bits, rowB0, I, 8 * (wv & 1), doD, cdn, lane, a.x);
+        fmm_issue_sb<8>(s.ds, s.db, rowB0, I, 8 * (wv & 1), doD, sdn, bdn, lane, a.x);
+    } else {
+        fmm_issue_codes(s.dw, bits, rowB0, I, 0, doD, cdn, lane, a.x);
+        fmm_issue_sb(s.ds, s.db, rowB0, I, 0, doD, sdn, bdn, lane, a.x);
+    }
     if (tid < 64) {  // wave 0 builds the quarter's 16 operand groups
         const int gg = tid >> 2, qq = tid & 3;
         float v[16];
@@ -1678,20 +1684,39 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     }
+    float y = 0.f;
     if (doD) {
         FM_DX_MARK(5);
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
-        if (bits == 4)
-            fmm_mma<4>(cdn, &L.aq[ys][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
-        else
-            fmm_mma<2>(cdn, &L.aq[ys][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
-        const float y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[ys][4 * q], &L.ainv[ys][4 * q]));
-        if (lane < 16) {
-            if (a.mode == 1)
-                a.expert_out[(size_t)ys * H + rowB0 + n] = y;
+        if (solo) {
+            // half h of the 16 groups (NG = 8: lanes q < 2 hold its groups)
+            const int h = wv & 1;
+            const fm_h2 *aq = &L.aq[0][bits == 4 ? 0 : 1][8 * h][0];
+            if (bits == 4)
+                fmm_mma<4, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
             else
-                L.y[ys][n] = y;
+                fmm_mma<2, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
+            const bool qok = q < 2;
+            const int gq = 8 * h + 4 * (qok ? q : 0);
+            y = fmm_q_sum(qok ? fmm_fold(d0 + d1, sdn, bdn, &L.asum[0][gq], &L.ainv[0][gq]) : 0.f);
+        } else {
+            if (bits == 4)
+                fmm_mma<4>(cdn, &L.aq[ys][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
+            else
+                fmm_mma<2>(cdn, &L.aq[ys][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
+            y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[ys][4 * q], &L.ainv[ys][4 * q]));
         }
+    }
+    if (solo && s.valid) {
+        if (wv == 3 && lane < 16) L.pu[n] = y;  // the second half, to wave 2
+        __syncthreads();
+        if (wv == 2) y += L.pu[n];
+    }
+    if (doD && (!solo || wv == 2) && lane < 16) {
+        if (a.mode == 1)
+            a.expert_out[(size_t)ys * H + rowB0 + n] = y;
+        else
+            L.y[ys][n] = y;
     }
     FM_DX_MARK(6);
     __syncthreads();
