@@ -1462,7 +1462,8 @@ struct __attribute__((aligned(16))) FmsLds {
     float asum[FMS_MAXS][FMM_GI], ainv[FMS_MAXS][FMM_GI];
     float act[FMS_MAXS][FMM_MAXI];
     float y[FMS_MAXS][16];
-    float pu[16];                 // one slot: the up wave's folded partials
+    float pu[16];                 // one slot: the second half of the down rows
+    float ph[4][16];              // one slot: each wave's half of the gate / up partials
     uint32_t tr[4][16 * FMM_TS];
 };
 
@@ -1488,15 +1489,25 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const FmSlot s = fmc_slot(a, mine ? wv : 0);
     const bool doA = mine && s.valid;
     const int bits = s.valid ? s.bits : 4;
-    const bool doG = solo ? s.valid && wv == 0 : doA, doU = solo ? s.valid && wv == 1 : doA;
+    // one slot: waves 0, 1 take the gate rows' input groups 0-7, 8-15 of the
+    // quarter, waves 2, 3 the up rows'
+    const bool doG = solo ? s.valid && wv < 2 : doA, doU = solo ? s.valid && wv >= 2 : doA;
+    const uint32_t gA = 16 * quarter + (solo ? 8 * (wv & 1) : 0);
     const bool doD = solo ? s.valid && wv >= 2 : doA;  // one slot: waves 2, 3 take down groups 0-7, 8-15
     const int ys = solo ? 0 : wv;  // the slot of this wave's down rows
     FmmCodes cg, cu, cdn;
     fmm_u2 sg, bg, su, bu, sdn, bdn;
-    fmm_issue_codes(s.gw, bits, rowA0, H, 16 * quarter, doG, cg, lane, a.x);
-    fmm_issue_sb(s.gs, s.gb, rowA0, H, 16 * quarter, doG, sg, bg, lane, a.x);
-    fmm_issue_codes(s.uw, bits, rowA0, H, 16 * quarter, doU, cu, lane, a.x);
-    fmm_issue_sb(s.us, s.ub, rowA0, H, 16 * quarter, doU, su, bu, lane, a.x);
+    if (solo) {
+        fmm_issue_codes<8>(s.gw, bits, rowA0, H, gA, doG, cg, lane, a.x);
+        fmm_issue_sb<8>(s.gs, s.gb, rowA0, H, gA, doG, sg, bg, lane, a.x);
+        fmm_issue_codes<8>(s.uw, bits, rowA0, H, gA, doU, cu, lane, a.x);
+        fmm_issue_sb<8>(s.us, s.ub, rowA0, H, gA, doU, su, bu, lane, a.x);
+    } else {
+        fmm_issue_codes(s.gw, bits, rowA0, H, gA, doG, cg, lane, a.x);
+        fmm_issue_sb(s.gs, s.gb, rowA0, H, gA, doG, sg, bg, lane, a.x);
+        fmm_issue_codes(s.uw, bits, rowA0, H, gA, doU, cu, lane, a.x);
+        fmm_issue_sb(s.us, s.ub, rowA0, H, gA, doU, su, bu, lane, a.x);
+    }
     if (solo) {
         fmm_issue_codes<8>(s.dw, bits, rowB0, I, 8 * (wv & 1), doD, cdn, lane, a.x);
         fmm_issue_sb<8>(s.ds, s.db, rowB0, I, 8 * (wv & 1), doD, sdn, bdn, lane, a.x);
@@ -1549,26 +1560,41 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     // ---- A: this quarter's partial gate/up sums of the 16 rows ----
     uint64_t *part = a.p2 + ((size_t)wv * (H / 64) + tile) * 4 * 32;  // [slot][tile][quarter][16 rows][g, u]
     float pg = 0.f, pu = 0.f;
-    if (doG || doU) {
+    if (solo && s.valid) {
+        // half h of the quarter's 16 groups of the gate (waves 0, 1) or up
+        // (waves 2, 3) rows; the four halves meet in LDS
+        const int h = wv & 1;
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][8 * h][0];
+        if (bits == 4)
+            fmm_mma<4, 8>(wv < 2 ? cg : cu, xq, L.zero, L.tr[wv], d0, d1, lane);
+        else
+            fmm_mma<2, 8>(wv < 2 ? cg : cu, xq, L.zero, L.tr[wv], d0, d1, lane);
+        FM_DX_MARK(2);
+        const bool qok = q < 2;
+        const int gq = 8 * h + 4 * (qok ? q : 0);
+        const float ph = fmm_q_sum(qok ? fmm_fold(d0 + d1, wv < 2 ? sg : su, wv < 2 ? bg : bu, &L.xsum[gq],
+                                                  &L.xinv[gq])
+                                       : 0.f);
+        if (lane < 16) L.ph[wv][lane] = ph;
+        __syncthreads();
+        pg = L.ph[0][lane & 15] + L.ph[1][lane & 15];
+        pu = L.ph[2][lane & 15] + L.ph[3][lane & 15];
+    } else if (doA) {
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][0][0];
         if (bits == 4) {
-            if (doG) fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            if (doU) fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         } else {
-            if (doG) fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            if (doU) fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         }
         FM_DX_MARK(2);
-        if (doG) pg = fmm_q_sum(fmm_fold(g0 + g1, sg, bg, &L.xsum[4 * q], &L.xinv[4 * q]));
-        if (doU) pu = fmm_q_sum(fmm_fold(u0 + u1, su, bu, &L.xsum[4 * q], &L.xinv[4 * q]));
-        if (solo && doU && lane < 16) L.pu[lane] = pu;
+        pg = fmm_q_sum(fmm_fold(g0 + g1, sg, bg, &L.xsum[4 * q], &L.xinv[4 * q]));
+        pu = fmm_q_sum(fmm_fold(u0 + u1, su, bu, &L.xsum[4 * q], &L.xinv[4 * q]));
     }
-    if (solo && s.valid) {
-        __syncthreads();  // the up wave's partials
-        if (doG) pu = L.pu[lane & 15];
-    }
-    if (doG) {
+    if (solo ? s.valid && wv == 0 : doA) {
         // lanes 0..15: gate of row n, lanes 16..31: up of row n - 16 (the
         // shuffle runs in the full wave: an inactive source lane reads as 0)
         const float pu_n = __shfl(pu, (lane - 16) & 63, 64);
