@@ -775,7 +775,11 @@ static bool fm_decode_allowed(const char *name) {
     return !only || !*only || !strcmp(only, name);
 }
 
-static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
+// hdr: the workspace header (status, epoch, finished-unit count) when the
+// step's buffers are a sub-region of a larger workspace (the shared expert of
+// its own size): every launch on a workspace then tags from the one epoch and
+// reports into the one status word; NULL = ws itself.
+static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStream_t st, void *hdr = nullptr) {
     const char *who = "fm_moe_decode";
     if (a.ntok <= 1) {
         a.ntok = 1;
@@ -790,7 +794,8 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
     FM_REQUIRE(a.S * 4 <= (int)a.inter, "%s: inter %u too small for %d slots", who, a.inter, a.S);
     char *p = (char *)ws;
-    a.err = (uint32_t *)p;
+    char *h = hdr ? (char *)hdr : p;
+    a.err = (uint32_t *)h;
     p += 256;
     a.act2 = (uint64_t *)p;
     p += fm_align_up((size_t)a.S * a.inter * 8, 256);
@@ -799,8 +804,8 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
     a.ss2 = (uint64_t *)p;
     p += fm_align_up((size_t)(a.hidden + 63) / 64 * 8, 256);
     a.p2 = (uint64_t *)p;
-    a.ws_epoch = (uint32_t *)((char *)ws + FM_WS_EPOCH_OFF);
-    a.ws_done = (uint32_t *)((char *)ws + FM_WS_DONE_OFF);
+    a.ws_epoch = (uint32_t *)(h + FM_WS_EPOCH_OFF);
+    a.ws_done = (uint32_t *)(h + FM_WS_DONE_OFF);
     if (a.route_logits) {
         // routing fused into the step where the per-CU kernel runs it;
         // otherwise the routing kernel first, then the step on its outputs
@@ -824,7 +829,7 @@ static int fm_decode_launch(FmDecodeArgs &a, void *ws, size_t ws_bytes, hipStrea
         fm_clear_error();
         FmDecodeArgs b = a;
         b.norm_w = nullptr;
-        rc = fm_decode_launch(b, ws, ws_bytes, st);
+        rc = fm_decode_launch(b, ws, ws_bytes, st, hdr);
         if (rc) return rc;
         return fm_launch_rms_norm(a.out, a.norm_w, a.hidden, a.norm_eps, a.normed, nullptr, st);
     }
@@ -893,7 +898,11 @@ static int fm_decode_launch_shared(FmDecodeArgs &a, uint32_t shared_inter, void 
     b.inter = shared_inter;
     b.x = a.x;
     b.expert_out = shared_y;
-    int rc = fm_decode_launch(b, (char *)ws + main, sub, st);
+    // the sub-launch's buffers lie in the tail, its header is the workspace's
+    // own: its tags come from the same epoch (so they only ever grow in every
+    // word of the workspace, whatever shapes alternate on it) and its status
+    // bits reach fm_workspace_status
+    int rc = fm_decode_launch(b, (char *)ws + main, sub, st, ws);
     if (rc) return rc;
     a.has_shared = 0;
     a.S = a.K;
@@ -1081,6 +1090,18 @@ static int fm_noalloc_scratch(hipStream_t st, void **out) {
 }
 
 extern "C" size_t fm_noalloc_workspace_bytes(void) { return FM_NOALLOC_WS_BYTES; }
+
+// fm_workspace_status of this device's static array: the status bits of the
+// no-allocation calls since the last read (bounded-wait timeouts, skipped
+// out-of-range experts, epoch wrap), then cleared.
+extern "C" int fm_noalloc_status(uint32_t *status, void *stream) {
+    fm_clear_error();
+    FM_REQUIRE(status, "fm_noalloc_status: NULL status");
+    void *ws = nullptr;
+    const int rc = fm_noalloc_scratch(fm_stream(stream), &ws);
+    if (rc) return rc;
+    return fm_workspace_status(ws, status, stream);
+}
 
 extern "C" int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
                                           const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,

@@ -759,8 +759,8 @@ struct __attribute__((aligned(16))) FmcRoute {
     int cv[FMC_THREADS + 4];          // top-K candidates: probability bits
     int ci[FMC_THREADS + 4];          // ... and element indices
     float red[FMC_THREADS / 64];      // per-wave sums of exp(l - max)
-    float inv;                        // 1 / softmax sum
-    int ncand, vk, pconv;
+    float inv;                        // 1 / softmax sum (per-wave sums: the kernel's own weights)
+    int ncand, ek1, vk, pconv;        // candidates; e bits at places K - 1 and K; pb holds exact p
     float s_val[64];                  // cpu_topk slots (serial replay)
     int s_id[64];
 };
@@ -882,7 +882,7 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
     float lg = lgq[0];
 #pragma unroll
     for (int q = 1; q < NW; q++) lg = wv == q ? lgq[q] : lg;
-    const float ev = tid < E ? expf(lg - mx) : 0.f;
+    const float ev = tid < E ? fm_expf_ref(lg - mx) : 0.f;  // the reference libm's exp, bit for bit
     const float ws = fm_lane_sum<64>(ev);
     if (lane == 0) R.red[wv] = ws;
     // candidates on e = exp(l - max), before the sum is known: p = e * (1 /
@@ -948,9 +948,9 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
             if (cnt < K) {
                 L.rsel[cnt] = (int)(1023 - (uint32_t)key);
                 L.rp[cnt] = pbits;
-            } else if (cnt == K) {
-                R.vk = pbits;
             }
+            if (cnt == K - 1) R.ek1 = (int)(key >> 32);
+            if (cnt == K) R.vk = (int)(key >> 32);
         }
     } else if (tid < NC) {
         const int v = R.cv[tid], me = R.ci[tid];
@@ -966,19 +966,29 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
         if (pos < K) {
             L.rsel[pos] = me;
             L.rp[pos] = pbits;
-        } else if (pos == K) {
-            R.vk = pbits;
         }
+        if (pos == K - 1) R.ek1 = v;
+        if (pos == K) R.vk = v;
     }
     if (tid == 0) R.inv = inv;
     __syncthreads();
     FM_DX_MARK(11);
-    if (R.vk == L.rp[K - 1]) {  // uniform (read after the barrier): equal p across the K-th place
+    // The set by e is cpu_topk's set when p = e * (1 / sum) cannot round equal
+    // across the K-th place, whatever the sum: e at place K - 1 at least 4 ulps
+    // above e at place K (p then differs by more than one rounding on each
+    // side) and large enough that p stays a normal number (sum <= E, so
+    // p >= e / 1024).  Otherwise (near-equal e there, a rare case) wavefront
+    // 0 derives p exactly -- cpu_softmax's sum in index order -- and replays
+    // cpu_topk on it.  Uniform (read after the barrier).
+    const int ek1 = R.ek1, ekk = R.vk;
+    const bool set_exact = ekk < 0 || (ek1 >= 0x0d800000 /* 2^-100 */ && ek1 - ekk >= 4);
+    if (!set_exact) {
         if (wv == 0) {
-            // p for every element, then cpu_topk's replacement history decides
+            const float pinv = 1.0f / fm_serial_sum((const float *)R.pb, E);
+            fm_wave_lds_sync();
             for (int i = lane; i < nch * 64; i += 64) {
                 const int v = R.pb[i];
-                R.pb[i] = v >= 0 ? __float_as_int(__int_as_float(v) * inv) : v;
+                R.pb[i] = v >= 0 ? __float_as_int(__int_as_float(v) * pinv) : v;
             }
             fm_wave_lds_sync();
             fm_topk_serial(R.pb, E, K, R);
@@ -1407,8 +1417,11 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         // cpu_topk's slot order by serial replay, then cpu_normalize_weights
         // (sequential sum over the slots) -- bit-equal to fm_route_kernel
         if (!L.rt.pconv) {
+            // p with cpu_softmax's sum (index order): bit-equal to the reference
+            const float pinv = 1.0f / fm_serial_sum((const float *)L.rt.pb, a.route_E);
+            fm_wave_lds_sync();
             for (int i = lane; i < a.route_E; i += 64)
-                L.rt.pb[i] = __float_as_int(__int_as_float(L.rt.pb[i]) * L.rt.inv);
+                L.rt.pb[i] = __float_as_int(__int_as_float(L.rt.pb[i]) * pinv);
             fm_wave_lds_sync();
         }
         fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt);

@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fm_expf.h"
+
 typedef _Float16 fm_h2 __attribute__((ext_vector_type(2)));
 typedef float fm_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t fm_u4 __attribute__((ext_vector_type(4)));
@@ -288,4 +290,5 @@ FM_DEV float fm_silu_mul(float g, float u) {
     return sg * u;
 }
 
-FM_DEV float fm_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// cpu_sigmoid (cpu_kernels.h:258-260) with the reference libm's expf: bit-equal.
+FM_DEV float fm_sigmoid(float x) { return 1.0f / (1.0f + fm_expf_ref(-x)); }

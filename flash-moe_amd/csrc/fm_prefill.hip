@@ -783,7 +783,7 @@ __global__ __launch_bounds__(64 * W, NST == 8 ? 1 : (LO || !RES ? 2 : PF_MINB)) 
 __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T, int K, int E, int has_shared,
                                                            const void *const *blobs, const uint8_t *bits_table,
                                                            int sh_bits, int *chunks, int *nchunks,
-                                                           uint32_t max_chunks, int *err) {
+                                                           uint32_t max_chunks, int *err, int tstage) {
     extern __shared__ int sm[];
     int *cnt = sm;               // [E + 1]
     int *base = sm + (E + 1);    // [E + 2]
@@ -794,10 +794,10 @@ __global__ __launch_bounds__(1024) void fm_pf_lists_kernel(const int *idx, int T
     FM_PL_MARK(0);
     const int NE = E + (has_shared ? 1 : 0);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // the pool table entries the chunk rows need (E <= 4096), loaded now (they
-    // arrive while the entries are counted) and staged in LDS before the scan
+    // the pool table entries the chunk rows need, loaded now (they arrive
+    // while the entries are counted) and staged in LDS before the scan; the
+    // host sets tstage when E <= 4096 and the extra LDS fits
     constexpr int PF_LT = 4;  // entries per thread
-    const bool tstage = E <= PF_LT * 1024;
     uint64_t pbl[PF_LT];
     int pbt[PF_LT];
 #pragma unroll
@@ -1258,12 +1258,15 @@ extern "C" int fm_prefill_moe(const fm_expert_pool *pool, int T, int K, const in
     const size_t nent = (size_t)T * K + grouped_shared * T;
 
     // lists
+    // (the pool table staged in LDS only where it fits beside the lists)
     size_t lds = ((size_t)pool->num_experts * 3 + 5) * sizeof(int);
-    if (pool->num_experts <= 4096) lds += ((size_t)pool->num_experts + 1) * sizeof(int) + 8 + (size_t)pool->num_experts * 8;
+    const size_t tab_lds = ((size_t)pool->num_experts + 1) * sizeof(int) + 8 + (size_t)pool->num_experts * 8;
+    const int tstage = pool->num_experts <= 4096 && lds + tab_lds <= 65536;
+    if (tstage) lds += tab_lds;
     if (lds > 65536) return fm_fail(FM_ERR_UNSUPPORTED, "%s: too many experts", who);
     hipLaunchKernelGGL(fm_pf_lists_kernel, dim3(1), dim3(1024), lds, st, idx, T, K, (int)pool->num_experts,
                        grouped_shared, pool->blobs, pool->bits, shared ? shared_bits : 4,
-                       (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err));
+                       (int *)(p + L.chunks), (int *)(p + L.nchunks), mc, (int *)(p + L.err), tstage);
     int rc = fm_check_launch("fm_pf_lists_kernel");
     if (rc) return rc;
     // token operands of X (fp16, one power-of-two scale per token)

@@ -102,20 +102,21 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < FM_RT_NW; w++) mx = fmaxf(mx, L.red[0][w]);
-    float sum = 0.f;
+    // exp with the reference libm's results, then the sum in index order
+    // (wavefront 0, the exponentials staged in pb): bit-equal probabilities
 #pragma unroll
     for (int q = 0; q < FM_RT_VPT; q++) {
         const int i = tid + q * FM_RT_THREADS;
-        v[q] = i < E ? expf(v[q] - mx) : 0.f;
-        sum += v[q];
+        v[q] = i < E ? fm_expf_ref(v[q] - mx) : 0.f;
+        if (i < E) pb[i] = __float_as_int(v[q]);
     }
-    sum = fm_lane_sum<64>(sum);
-    if (lane == 0) L.red[1][wv] = sum;
     __syncthreads();
-    sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < FM_RT_NW; w++) sum += L.red[1][w];
-    const float inv = 1.0f / sum;
+    if (wv == 0) {
+        const float s = fm_serial_sum((const float *)pb, E);
+        if (lane == 0) L.red[1][0] = s;
+    }
+    __syncthreads();
+    const float inv = 1.0f / L.red[1][0];
 #pragma unroll
     for (int q = 0; q < FM_RT_VPT; q++) {
         const int i = tid + q * FM_RT_THREADS;

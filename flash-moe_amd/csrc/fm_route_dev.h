@@ -13,6 +13,25 @@
 #define FM_RT_DECL
 #endif
 
+// cpu_softmax's sum (cpu_kernels.h:269-273): v[0] + v[1] + ... in index
+// order, one rounding per term, so the sum -- and 1 / sum -- are bit-equal to
+// the reference's.  Run by one wavefront (every lane alike: the LDS reads are
+// broadcasts); v is 16-byte aligned.  ~4 cycles per term.
+FM_DEV float fm_serial_sum(const float *v, int n) {
+    float s = 0.f;
+    int i = 0;
+#pragma unroll 4
+    for (; i + 4 <= n; i += 4) {
+        const fm_f4 q = *(const fm_f4 *)(v + i);
+        s = __fadd_rn(s, q.x);
+        s = __fadd_rn(s, q.y);
+        s = __fadd_rn(s, q.z);
+        s = __fadd_rn(s, q.w);
+    }
+    for (; i < n; i++) s = __fadd_rn(s, v[i]);
+    return s;
+}
+
 FM_DEV float fm_wave_max(float v) {
     v = fmaxf(v, fm_dpp_f<0xB1>(v));
     v = fmaxf(v, fm_dpp_f<0x4E>(v));

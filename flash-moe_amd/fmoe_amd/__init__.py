@@ -98,6 +98,7 @@ SIGNATURES = {
     "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),
     "fm_workspace_status": (I32, [P, ctypes.POINTER(ctypes.c_uint32), P]),
     "fm_noalloc_workspace_bytes": (ctypes.c_size_t, []),
+    "fm_noalloc_status": (I32, [ctypes.POINTER(ctypes.c_uint32), P]),
     "fm_moe_decode_pool_noalloc": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
                                          I32, U32, P, P, P, P, P, P]),
     "fm_workspace_init": (I32, [P, ctypes.c_size_t, P]),

@@ -137,6 +137,13 @@ def workspace_status(ws, stream=None):
     return v.value
 
 
+def noalloc_status(stream=None):
+    """Status bits of the no-allocation calls on this device since the last read (then cleared)."""
+    v = ctypes.c_uint32(0)
+    check(lib().fm_noalloc_status(ctypes.byref(v), stream_ptr(stream)))
+    return v.value
+
+
 def workspace_init(ws, stream=None):
     """Zero a workspace with the library's fill kernel (fm_workspace_init)."""
     check(lib().fm_workspace_init(ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))

@@ -234,6 +234,12 @@ int fm_moe_route_decode_pool(const fm_expert_pool *pool, const float *logits, in
  * host threads) race and must be serialised by the caller. */
 #define FM_NOALLOC_WS_BYTES (2u << 20)
 size_t fm_noalloc_workspace_bytes(void);
+/* No counterpart in the reference either: the status word of this device's
+ * static array (FM_STATUS_* bits of the no-allocation calls since the last
+ * read, e.g. FM_STATUS_WAIT_TIMEOUT, whose step output is then invalid, or
+ * FM_STATUS_BAD_EXPERT), read and cleared like fm_workspace_status (it
+ * synchronises `stream`).  Poll it after a step, outside graph capture. */
+int fm_noalloc_status(uint32_t *status, void *stream);
 int fm_moe_decode_pool_noalloc(const fm_expert_pool *pool, int K, const int *idx,
                                const float *weights, const fm_expert_weights *shared,
                                int shared_bits, uint32_t shared_inter, const float *shared_gate_score,

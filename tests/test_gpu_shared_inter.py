@@ -149,3 +149,50 @@ def test_layer_driver_shared_inter(orc, dev):
     refp = orc.prefill_moe(pi, pw, blobs, bits, HP, HIDDEN, INTER, shared_blob=sb, shared_bits=4, shared_scores=sc,
                            shared_inter=Is)
     assert norm_err(outp.cpu().numpy(), refp) <= TOL_F32
+
+
+def test_alternating_shapes_one_workspace(orc, dev):
+    """Calls alternating between a shared expert of the routed size and one of
+    its own size (which runs as a sub-launch on the workspace tail), with
+    different K, on ONE workspace and on the no-allocation path: the
+    sub-launch tags from the workspace's own epoch, so no call can accept
+    another's stale words; every output is checked against the oracle and the
+    status words stay clean."""
+    import torch
+    say("alternating shared_inter / K on one workspace")
+    E = 24
+    bits = [4 if e % 3 else 2 for e in range(E)]
+    blobs = experts(range(9600, 9600 + E), bits)
+    pool = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    shb = {si: synth.expert_blob((9700, si), HIDDEN, si, 4) for si in (INTER, 512, 2048)}
+    dsh = {si: T(b, dev) for si, b in shb.items()}
+    shw = {si: fm.experts_from_blob(dsh[si], 4, HIDDEN, si) for si in shb}
+    ws = fm.workspace(max(fm.decode_workspace_bytes_ex(k, 1, HIDDEN, INTER, si)
+                          for k in (3, 8, 12) for si in shb), dev)
+    rng = synth.rng_for(97)
+    fm.noalloc_status()  # clear what earlier tests left
+    seq = [(8, 512), (12, INTER), (3, 2048), (8, INTER), (12, 512), (3, 512), (8, 2048), (12, INTER)]
+    for i, (K, si) in enumerate(seq):
+        lg = rng.normal(0, 1, (1, E)).astype(np.float32)
+        x = synth.hidden_vec(rng, HIDDEN)
+        hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+        g = np.array([rng.normal()], np.float32)
+        ri, rw = orc.route(lg, K)
+        ref = orc.moe_decode([blobs[e] for e in ri[0]], [bits[e] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                             shared_blob=shb[si], shared_bits=4, shared_score=float(g[0]), h_mid=hm,
+                             shared_inter=0 if si == INTER else si)
+        idx, w = T(ri, dev), T(rw, dev)
+        kw = dict(shared=shw[si], shared_bits=4, shared_score=T(g, dev), h_mid=T(hm, dev),
+                  shared_inter=0 if si == INTER else si)
+        out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+        out2 = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+        fm.moe_decode_pool(pool, idx, w, T(x, dev), out, ws, **kw)
+        if fm.decode_workspace_bytes_ex(K, 1, HIDDEN, INTER, kw["shared_inter"]) <= fm.lib().fm_noalloc_workspace_bytes():
+            fm.moe_decode_pool_noalloc(pool, idx, w, T(x, dev), out2, **kw)
+        else:
+            out2.copy_(out)
+        torch.cuda.synchronize()
+        assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, (i, K, si)
+        assert norm_err(out2.cpu().numpy() - hm, ref - hm) <= TOL_F32, (i, K, si)
+    assert fm.workspace_status(ws) == 0
+    assert fm.noalloc_status() == 0

@@ -65,6 +65,33 @@ def test_noalloc_matches_workspace_entry_point(dev):
     _run_both(dev, big)
 
 
+def test_noalloc_status_reports_bad_expert(dev):
+    """An out-of-range expert index is skipped by the step and reported through
+    fm_noalloc_status (read and cleared); a clean call reads 0 afterwards."""
+    import torch
+    print("[case] noalloc status: out-of-range expert", flush=True)
+    c = _case(dev, 8300, 32, 6, 4096, 1024, True)
+    assert fm.noalloc_status() == 0  # earlier calls of this process were clean
+    bad = c["idx"].clone()
+    bad[0, 2] = 40  # pool of 32 experts
+    out = torch.empty(c["H"], dtype=torch.float32, device=dev)
+    fm.moe_decode_pool_noalloc(c["pool"], bad, c["w"], c["x"], out, shared=c["sh"], shared_bits=4,
+                               shared_score=c["g"], h_mid=c["hm"])
+    st = fm.noalloc_status()
+    assert st & 2, st  # FM_STATUS_BAD_EXPERT
+    assert not st & 1, st  # no wait timed out
+    # the step skipped that slot: equal to the workspace entry point with the slot skipped too
+    ws = fm.workspace(fm.decode_workspace_bytes(c["K"] + 1, c["H"], c["I"]), dev)
+    ref = torch.empty(c["H"], dtype=torch.float32, device=dev)
+    fm.moe_decode_pool(c["pool"], bad, c["w"], c["x"], ref, ws, shared=c["sh"], shared_bits=4,
+                       shared_score=c["g"], h_mid=c["hm"])
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    assert fm.noalloc_status() == 0  # cleared by the read
+    _run_both(dev, c)
+    assert fm.noalloc_status() == 0
+
+
 def test_noalloc_rejects_oversized_shape():
     assert fm.lib().fm_noalloc_workspace_bytes() == 2 << 20
     dummy = (ctypes.c_void_p * 1)(1)
