@@ -1053,6 +1053,112 @@ extern "C" int fm_moe_route_decode_pool(const fm_expert_pool *pool, const float 
                                h_mid, out, out_bf16, nullptr, 0.f, nullptr, ws, ws_bytes, stream, 1, logits, E);
 }
 
+// ------------------------------------------------------- step by step --
+// fm_moe_decode_pool_stepwise: the decode step as a chain of launches that
+// never wait on one another (batched gate/up matvecs, SwiGLU, per-slot down
+// matvecs, the combine): no workgroup depends on another being resident, so
+// it completes whatever else occupies the GPU.  The recovery path of the layer
+// driver after FM_STATUS_WAIT_TIMEOUT (fm_moe_forward_checked); it reads the
+// routing on the host, so it synchronises `stream`.  The workspace is the
+// step's own (fm_moe_decode_workspace_size_ex), used as plain scratch and
+// re-initialised (fm_workspace_init) at the end.
+extern "C" int fm_moe_decode_pool_stepwise(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
+                                           const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
+                                           const float *shared_gate_score, const float *x, const float *h_mid,
+                                           float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream) {
+    const char *who = "fm_moe_decode_pool_stepwise";
+    fm_clear_error();
+    FM_REQUIRE(pool && pool->blobs && pool->bits && pool->num_experts, "%s: invalid pool", who);
+    FM_REQUIRE(K >= 0 && K <= FM_MAX_K, "%s: K=%d outside 0..%d", who, K, FM_MAX_K);
+    FM_REQUIRE(K == 0 || (idx && weights), "%s: NULL idx/weights", who);
+    FM_REQUIRE(K > 0 || shared, "%s: no experts", who);
+    FM_REQUIRE(x && out && ws, "%s: NULL x, out or workspace", who);
+    if (pool->group_size != 64) return fm_fail(FM_ERR_UNSUPPORTED, "%s: group_size must be 64", who);
+    const uint32_t H = pool->hidden, I = pool->inter, Is = shared_inter ? shared_inter : I;
+    const int S = K + (shared ? 1 : 0);
+    const size_t need = fm_moe_decode_workspace_size_ex(K, shared ? 1 : 0, H, I, shared ? shared_inter : 0);
+    const size_t scratch_bytes = 256 + fm_align_up(((size_t)K * 3 * I + (shared ? 3 * (size_t)Is : 0) +
+                                                    (size_t)S * H + (size_t)K) * 4, 256);
+    if (ws_bytes < need || ws_bytes < scratch_bytes)
+        return fm_fail(FM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu required", who, ws_bytes,
+                       need > scratch_bytes ? need : scratch_bytes);
+    if ((uintptr_t)ws & 255) return fm_fail(FM_ERR_INVALID, "%s: workspace not 256-byte aligned", who);
+    hipStream_t st = fm_stream(stream);
+    // the routing and the selected experts' table entries, on the host
+    int hidx[FM_MAX_K] = {0}, hvalid[FM_MAX_K] = {0};
+    fm_expert_weights ew[FM_MAX_SLOTS];
+    int ebits[FM_MAX_SLOTS];
+    hipError_t e = K ? hipMemcpyAsync(hidx, idx, sizeof(int) * K, hipMemcpyDeviceToHost, st) : hipSuccess;
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    fm_expert_layout l4, l2;
+    fm_expert_layout_compute(H, I, 64, 4, &l4);
+    fm_expert_layout_compute(H, I, 64, 2, &l2);
+    for (int k = 0; k < K && e == hipSuccess; k++) {
+        if (hidx[k] < 0 || (uint32_t)hidx[k] >= pool->num_experts) continue;  // skipped, as in the one-launch step
+        const void *blob = nullptr;
+        uint8_t b = 0;
+        e = hipMemcpy(&blob, pool->blobs + hidx[k], sizeof blob, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(&b, pool->bits + hidx[k], 1, hipMemcpyDeviceToHost);
+        if (e == hipSuccess && blob && (b == 2 || b == 4)) {
+            fm_expert_from_blob(blob, b == 2 ? &l2 : &l4, &ew[k]);
+            ebits[k] = b;
+            hvalid[k] = 1;
+        }
+    }
+    if (e != hipSuccess) return fm_fail(FM_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
+    if (shared) {
+        int rc = fm_check_expert(who, K, *shared, shared_bits);
+        if (rc) return rc;
+        ew[K] = *shared;
+        ebits[K] = shared_bits;
+    }
+    // scratch after the header: gate / up / act per slot, then y [S][H], then valid [K]
+    float *g = (float *)((char *)ws + 256);
+    float *gs[FM_MAX_SLOTS], *us[FM_MAX_SLOTS], *as[FM_MAX_SLOTS];
+    {
+        float *q = g;
+        for (int k = 0; k < S; k++) {
+            const uint32_t ik = k < K ? I : Is;
+            gs[k] = q;
+            us[k] = q + ik;
+            as[k] = q + 2 * ik;
+            q += 3 * ik;
+        }
+        g = q;
+    }
+    float *y = g;
+    int *dvalid = (int *)(y + (size_t)S * H);
+    fm_batch_matvec_spec specs[2 * FM_MAX_SLOTS];
+    int ns = 0;
+    for (int k = 0; k < S; k++) {
+        if (k < K && !hvalid[k]) continue;
+        const uint32_t ik = k < K ? I : Is;
+        specs[ns++] = {ew[k].gate_w, ew[k].gate_s, ew[k].gate_b, gs[k], ik, H, 64, ebits[k]};
+        specs[ns++] = {ew[k].up_w, ew[k].up_s, ew[k].up_b, us[k], ik, H, 64, ebits[k]};
+    }
+    int rc = ns ? fm_batch_matvec(x, H, specs, ns, stream) : FM_OK;
+    for (int k = 0; k < S && !rc; k++) {
+        if (k < K && !hvalid[k]) continue;
+        const uint32_t ik = k < K ? I : Is;
+        rc = fm_swiglu(gs[k], us[k], as[k], ik, stream);
+        if (!rc)
+            rc = fm_dequant_matvec(ew[k].down_w, ew[k].down_s, ew[k].down_b, as[k], y + (size_t)k * H, H, ik, 64,
+                                   ebits[k], stream);
+    }
+    if (rc) return rc;
+    if (K) {
+        e = hipMemcpyAsync(dvalid, hvalid, sizeof(int) * K, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return fm_fail(FM_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
+    }
+    rc = fm_moe_combine(h_mid, y, weights, K ? dvalid : nullptr, K, shared ? y + (size_t)K * H : nullptr,
+                        shared ? shared_gate_score : nullptr, out, out_bf16, H, stream);
+    if (rc) return rc;
+    // hvalid is read by the copy above: wait for it before returning
+    e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return fm_fail(FM_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
+    return fm_workspace_init(ws, ws_bytes, stream);
+}
+
 // ------------------------------------------------- no-allocation variant --
 // fm_moe_decode_pool_noalloc: the same step with its workspace in a file-scope
 // device array (`scratch`, FM_NOALLOC_WS_BYTES per GPU, held until the process

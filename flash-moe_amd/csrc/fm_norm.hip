@@ -1,4 +1,5 @@
-// fm_norm.hip -- RMS norm with bf16 weights on the device.
+// fm_norm.hip -- RMS norm with bf16 weights, and the elementwise SwiGLU, on
+// the device.
 //
 // cpu_rms_norm (cpu_kernels.h:235-246) / rms_norm_sum_sq + rms_norm_apply_bf16
 // (shaders.metal:792-870) as used for the next layer's input norm at the end
@@ -42,4 +43,20 @@ extern "C" int fm_rms_norm(const float *x, const uint16_t *w, uint32_t dim, floa
     FM_REQUIRE(dim >= 1, "fm_rms_norm: dim 0");
     FM_REQUIRE(eps >= 0.f, "fm_rms_norm: eps < 0");
     return fm_launch_rms_norm(x, w, dim, eps, out, out_bf16, fm_stream(stream));
+}
+
+// act[i] = silu(gate[i]) * up[i] (cpu_swiglu, cpu_kernels.h:249-255; the
+// swiglu_fused kernel of shaders.metal:714-727), for the step-by-step decode.
+__global__ __launch_bounds__(256) void fm_swiglu_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                        float *__restrict__ act, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) act[i] = fm_silu_mul(g[i], u[i]);
+}
+
+extern "C" int fm_swiglu(const float *gate, const float *up, float *act, uint32_t n, void *stream) {
+    fm_clear_error();
+    FM_REQUIRE(gate && up && act, "fm_swiglu: NULL argument");
+    if (n == 0) return FM_OK;
+    hipLaunchKernelGGL(fm_swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, fm_stream(stream), gate, up, act, n);
+    return fm_check_launch("fm_swiglu_kernel");
 }

@@ -96,6 +96,9 @@ SIGNATURES = {
     "fm_moe_decode_pool_norm": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
                                       I32, U32, P, P, P, P, P, P, F32, P, P, SZ, P]),
     "fm_rms_norm": (I32, [P, P, U32, F32, P, P, P]),
+    "fm_swiglu": (I32, [P, P, P, U32, P]),
+    "fm_moe_decode_pool_stepwise": (I32, [ctypes.POINTER(ExpertPool), I32, P, P, ctypes.POINTER(ExpertWeights),
+                                          I32, U32, P, P, P, P, P, P, SZ, P]),
     "fm_workspace_status": (I32, [P, ctypes.POINTER(ctypes.c_uint32), P]),
     "fm_noalloc_workspace_bytes": (ctypes.c_size_t, []),
     "fm_noalloc_status": (I32, [ctypes.POINTER(ctypes.c_uint32), P]),
@@ -111,6 +114,8 @@ SIGNATURES = {
     "fm_moe_forward_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32]),
     "fm_moe_forward": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, SZ, P]),
     "fm_moe_forward_norm": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, F32, P, P, SZ, P]),
+    "fm_moe_forward_checked": (I32, [ctypes.POINTER(MoeLayer), I32, P, P, P, P, P, SZ, P,
+                                     ctypes.POINTER(ctypes.c_uint32)]),
     "fm_moe_prefill_workspace_size": (SZ, [ctypes.POINTER(MoeLayer), I32, I32]),
     "fm_moe_prefill_forward": (I32, [ctypes.POINTER(MoeLayer), I32, I32, P, P, P, P, P, SZ, P]),
     "fm_expert_store_open": (I32, [ctypes.c_char_p, I32, U32, U32, U32, U32, U32, I32,

@@ -18,9 +18,10 @@ __all__ = [
     "moe_decode_pool_norm", "rms_norm", "moe_forward_norm", "workspace_status",
     "STATUS_WAIT_TIMEOUT", "STATUS_BAD_EXPERT", "STATUS_CHUNKS", "STATUS_EPOCH_WRAP", "workspace_init",
     "workspace", "moe_decode_pool_noalloc", "decode_workspace_bytes_ex", "moe_route_decode_pool",
+    "noalloc_status", "moe_forward_checked", "moe_decode_pool_stepwise", "STATUS_RECOVERED",
 ]
 
-STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP = 1, 2, 4, 8
+STATUS_WAIT_TIMEOUT, STATUS_BAD_EXPERT, STATUS_CHUNKS, STATUS_EPOCH_WRAP, STATUS_RECOVERED = 1, 2, 4, 8, 16
 
 
 def _i32_array(vals):
@@ -238,6 +239,23 @@ def moe_forward_workspace_bytes(layer, K):
 def moe_forward(layer, K, h_post, h_mid, out, ws, out_bf16=None, stream=None):
     check(lib().fm_moe_forward(ctypes.byref(layer), K, ptr(h_post), ptr(h_mid), ptr(out), ptr(out_bf16),
                                ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream)))
+
+
+def moe_forward_checked(layer, K, h_post, h_mid, out, ws, out_bf16=None, stream=None):
+    """fm_moe_forward plus the status check and recovery; returns the FM_STATUS_* bits."""
+    st = ctypes.c_uint32(0)
+    check(lib().fm_moe_forward_checked(ctypes.byref(layer), K, ptr(h_post), ptr(h_mid), ptr(out), ptr(out_bf16),
+                                       ptr(ws), ws.numel() * ws.element_size(), stream_ptr(stream), ctypes.byref(st)))
+    return st.value
+
+
+def moe_decode_pool_stepwise(pool, idx, weights, x, out, ws, shared=None, shared_bits=4, shared_score=None,
+                             h_mid=None, out_bf16=None, stream=None, shared_inter=0):
+    K = idx.numel()
+    check(lib().fm_moe_decode_pool_stepwise(
+        ctypes.byref(pool.c), K, ptr(idx), ptr(weights), ctypes.byref(shared) if shared is not None else None,
+        shared_bits, shared_inter, ptr(shared_score), ptr(x), ptr(h_mid), ptr(out), ptr(out_bf16), ptr(ws),
+        ws.numel() * ws.element_size(), stream_ptr(stream)))
 
 
 def moe_forward_norm(layer, K, h_post, h_mid, out, ws, norm_w, eps, normed, out_bf16=None, stream=None):

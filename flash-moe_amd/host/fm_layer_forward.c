@@ -10,6 +10,7 @@
 #include "fm_layer_forward.h"
 
 #include <stdint.h>
+#include <stdlib.h>
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -92,6 +93,40 @@ int fm_moe_forward_norm(const fm_moe_layer *L, int K, const float *h_post, const
     if (!next_norm_w || !normed) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward_norm: NULL norm weights or output");
     return moe_forward_impl("fm_moe_forward_norm", L, K, h_post, h_mid, out, out_bf16, next_norm_w, eps, normed, ws,
                             ws_bytes, stream);
+}
+
+int fm_moe_forward_checked(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                           float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream,
+                           uint32_t *status) {
+    if (!status) return fm_host_fail(FM_ERR_INVALID, "fm_moe_forward_checked: NULL status");
+    int rc = moe_forward_impl("fm_moe_forward_checked", L, K, h_post, h_mid, out, out_bf16, NULL, 0.f, NULL, ws,
+                              ws_bytes, stream);
+    if (rc) return rc;
+    uint32_t st = 0;
+    rc = fm_workspace_status(ws, &st, stream); /* the step's region starts the workspace */
+    if (rc) return rc;
+    const char *force = getenv("FMOE_FORCE_STEP_RECOVERY");
+    if (force && force[0] == '1') st |= FM_STATUS_WAIT_TIMEOUT;
+    if (st & FM_STATUS_WAIT_TIMEOUT) {
+        /* the routing the step wrote (it needs no other workgroup) and the
+         * router outputs, in the workspace layout of moe_forward_impl */
+        const size_t step =
+            fm_moe_decode_workspace_size_ex(K, L->has_shared, L->pool.hidden, L->pool.inter, L->shared_inter);
+        char *p = (char *)ws + step;
+        p += align256((size_t)L->pool.num_experts * sizeof(float));
+        const float *seg = (const float *)p;
+        p += align256(sizeof(float));
+        const int *idx = (const int *)p;
+        p += align256((size_t)K * sizeof(int));
+        const float *w = (const float *)p;
+        rc = fm_moe_decode_pool_stepwise(&L->pool, K, idx, w, L->has_shared ? &L->shared : NULL, L->shared_bits,
+                                         L->shared_inter, L->has_shared ? seg : NULL, h_post, h_mid, out, out_bf16,
+                                         ws, step, stream);
+        if (rc) return rc;
+        st |= FM_STATUS_RECOVERED;
+    }
+    *status = st;
+    return FM_OK;
 }
 
 size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T) {

@@ -152,6 +152,7 @@ int fm_workspace_init(void *ws, size_t ws_bytes, void *stream);
 #define FM_STATUS_BAD_EXPERT 2u    /* a routed expert index outside the pool was skipped */
 #define FM_STATUS_CHUNKS 4u        /* prefill: more expert chunks than the workspace holds */
 #define FM_STATUS_EPOCH_WRAP 8u    /* the per-call tag wrapped after 2^32 - 1 calls: fm_workspace_init needed */
+#define FM_STATUS_RECOVERED 16u    /* fm_moe_forward_checked: the step timed out and was recomputed (output valid) */
 int fm_workspace_status(void *ws, uint32_t *status, void *stream);
 
 /* K expert FFNs sharing input x, one output per expert:
@@ -221,6 +222,25 @@ int fm_moe_route_decode_pool(const fm_expert_pool *pool, const float *logits, in
                              uint32_t shared_inter, const float *shared_gate_score, const float *x,
                              const float *h_mid, float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes,
                              void *stream);
+
+/* fm_moe_decode_pool as a chain of independent launches -- one batched
+ * gate/up matvec launch, per slot SwiGLU and down matvec, the weighted
+ * combine -- the way the reference's non-fused path runs an expert step
+ * (gpu_encode_experts_batched + moe_combine_residual, gpu_dispatch.h:461-609,
+ * shaders.metal:1865-1900).  No workgroup waits on another, so it completes
+ * even when the one-launch step could not have all its workgroups resident
+ * (FM_STATUS_WAIT_TIMEOUT); the layer driver's recovery path
+ * (fm_moe_forward_checked).  Reads the routing on the host: synchronises
+ * `stream`.  Same workspace as fm_moe_decode_pool (used as scratch, then
+ * re-initialised with fm_workspace_init). */
+int fm_moe_decode_pool_stepwise(const fm_expert_pool *pool, int K, const int *idx, const float *weights,
+                                const fm_expert_weights *shared, int shared_bits, uint32_t shared_inter,
+                                const float *shared_gate_score, const float *x, const float *h_mid,
+                                float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream);
+
+/* act[i] = silu(gate[i]) * up[i], n elements (cpu_swiglu, cpu_kernels.h:
+ * 249-255; swiglu_fused, shaders.metal:714-727).  Device fp32 arrays. */
+int fm_swiglu(const float *gate, const float *up, float *act, uint32_t n, void *stream);
 
 /* No counterpart in the reference: fm_moe_decode_pool for callers that cannot
  * allocate device memory (code recorded into a HIP graph, tight serving loops,

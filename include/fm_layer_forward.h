@@ -50,6 +50,20 @@ int fm_moe_forward_norm(const fm_moe_layer *L, int K, const float *h_post, const
                         uint16_t *out_bf16, const uint16_t *next_norm_w, float eps, float *normed, void *ws,
                         size_t ws_bytes, void *stream);
 
+/* fm_moe_forward, then a check of the step: *status receives the step's
+ * FM_STATUS_* bits (this call synchronises `stream`).  The one-launch step
+ * needs all of its workgroups resident at once; work from other streams or
+ * processes holding CUs for long can make a bounded wait give up
+ * (FM_STATUS_WAIT_TIMEOUT), leaving `out` invalid.  Then the step is
+ * recomputed with fm_moe_decode_pool_stepwise (independent launches, no
+ * residency needed) on the routing the first launch wrote, FM_STATUS_RECOVERED
+ * is added and the result is valid (an error code only if a call fails).
+ * FMOE_FORCE_STEP_RECOVERY=1 in the environment takes the recovery path on
+ * every call (to exercise it).  Same workspace as fm_moe_forward. */
+int fm_moe_forward_checked(const fm_moe_layer *L, int K, const float *h_post, const float *h_mid,
+                           float *out, uint16_t *out_bf16, void *ws, size_t ws_bytes, void *stream,
+                           uint32_t *status);
+
 size_t fm_moe_prefill_workspace_size(const fm_moe_layer *L, int K, int T);
 
 /* Prefill of T tokens: the MoE part of batched_prefill (batched_prefill.h:

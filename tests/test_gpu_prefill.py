@@ -159,11 +159,15 @@ def test_moe_prefill_forward_layer(orc, dev):
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
 
 
-def test_prefill_large_expert_count(orc, dev):
-    """2048 experts (blob table cycling over 8 blobs) through the grouped GEMM path."""
+@pytest.mark.parametrize("E", [2048, 3000, 4096, 5000])
+def test_prefill_large_expert_count(orc, dev, E):
+    """Large pools (blob table cycling over 8 blobs) through the grouped GEMM
+    path: 2048 (pool table staged in LDS by the lists kernel), 3000 and 4096
+    (the staged table would not fit beside the lists: read from memory) and
+    5000 (beyond the staging range)."""
     import torch
-    say("prefill E=2048")
-    E, Tn, K = 2048, 40, 6
+    say("prefill E", E)
+    Tn, K = 40, 6
     bits8 = [4, 2, 4, 4, 2, 4, 2, 4]
     blobs8 = experts(range(3600, 3608), bits8)
     dp = fm.DevicePool(blobs8, bits8, HIDDEN, INTER)

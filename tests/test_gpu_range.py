@@ -136,3 +136,69 @@ def test_pfb_gemm_range(orc, dev, bits, regime):
     got = Y.cpu().numpy()
     for t in range(N):
         assert norm_err(got[t], ref[t]) <= TOL_F32, t
+
+
+@pytest.mark.parametrize("regime", REGIMES)
+@pytest.mark.parametrize("K,bits", [(1, 4), (1, 2), (3, 4), (3, 2)])
+def test_decode_few_slots_range(orc, dev, regime, K, bits):
+    """One to three slots, no shared expert: the few-slot kernel (256
+    workgroups, quarter partials handed off, down rows over all activations;
+    with one slot its waves split the gate/up/down inputs), per-expert outputs
+    and the combine."""
+    import torch
+    say("decode few slots range", regime, K, bits)
+    bl = [bits] * K
+    blobs = experts(range(5400 + 10 * K + bits, 5400 + 10 * K + bits + K), bl)
+    rng = synth.rng_for(45, REGIMES.index(regime), K, bits)
+    x = x_regime(rng, HIDDEN, regime)
+    w = orc.route(rng.normal(0, 1, 16).astype(np.float32), K)[1][0]
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, bits, HIDDEN, INTER) for db in dblobs]
+    ws = fm.workspace(fm.decode_workspace_bytes(K, HIDDEN, INTER), dev)
+    eo = torch.zeros((K, HIDDEN), dtype=torch.float32, device=dev)
+    fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_decode(ex, bl, w, T(x, dev), out, ws, HIDDEN, INTER)
+    torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
+    eon = eo.cpu().numpy()
+    for k in range(K):
+        assert norm_err(eon[k], orc.expert_forward(blobs[k], bits, HIDDEN, INTER, x)) <= TOL_F32, k
+    ref = orc.moe_decode(blobs, bl, w, x, HIDDEN, INTER)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("regime", REGIMES)
+def test_route_decode_range(orc, dev, regime):
+    """The headline step: routing of 512 logits fused into the one-workgroup-
+    per-CU launch (top-10 + shared, 4- and 2-bit slots)."""
+    import torch
+    say("route+decode range", regime)
+    E, K, nb = 512, 10, 12
+    bits8 = [4, 2, 4, 4, 2, 4, 2, 4, 4, 2, 4, 4]
+    blobs = experts(range(5500, 5500 + nb), bits8)
+    dp = fm.DevicePool(blobs, bits8, HIDDEN, INTER)
+    dp.blob_table = T(np.array([dp.addrs[e % nb] for e in range(E)], np.int64), dev)
+    dp.bits_table = T(np.array([bits8[e % nb] for e in range(E)], np.uint8), dev)
+    dp.c = fm.ExpertPool(dp.blob_table.data_ptr(), dp.bits_table.data_ptr(), E, HIDDEN, INTER, 64)
+    rng = synth.rng_for(46, REGIMES.index(regime))
+    lg = rng.normal(0, 1, E).astype(np.float32)
+    x = x_regime(rng, HIDDEN, regime)
+    hm = (x_regime(rng, HIDDEN, regime) * 0.5).astype(np.float32)
+    g = np.array([0.3], np.float32)
+    sh_blob = synth.expert_blob((5600, 1), HIDDEN, INTER, 4)
+    dsh = T(sh_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    idx = torch.empty(K, dtype=torch.int32, device=dev)
+    w = torch.empty(K, dtype=torch.float32, device=dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_route_decode_pool(dp, T(lg, dev), idx, w, T(x, dev), out, ws, shared=sh, shared_bits=4,
+                             shared_score=T(g, dev), h_mid=T(hm, dev))
+    torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
+    ri, rw = orc.route(lg[None, :], K)
+    assert np.array_equal(idx.cpu().numpy(), ri[0])
+    ref = orc.moe_decode([blobs[e % nb] for e in ri[0]], [bits8[e % nb] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                         shared_blob=sh_blob, shared_bits=4, shared_score=float(g[0]), h_mid=hm)
+    assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32

@@ -163,3 +163,15 @@ def test_c_consumer_compiles_and_links(tmp_path):
     subprocess.run(cmd, check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 2 and "usage" in r.stderr
+
+
+def test_moe_forward_checked_rejects_before_launch():
+    """fm_moe_forward_checked validates its arguments on the host: a NULL
+    status pointer or an incomplete layer is refused before any GPU call."""
+    L = fmoe_amd.lib()
+    layer = fmoe_amd.MoeLayer()
+    st = ctypes.c_uint32(0)
+    assert L.fm_moe_forward_checked(ctypes.byref(layer), 8, 1, 1, 1, None, 1, 1 << 20, None, None) == -1
+    assert "NULL status" in L.fm_last_error().decode()
+    assert L.fm_moe_forward_checked(ctypes.byref(layer), 8, 1, 1, 1, None, 1, 1 << 20, None, ctypes.byref(st)) == -1
+    assert "incomplete layer" in L.fm_last_error().decode()
