@@ -661,6 +661,7 @@ struct __attribute__((aligned(16))) FmcItem {
     uint32_t tr[4][16 * FMM_TS];  // per-wave transpose buffers
     uint32_t scl[4][16][FMM_GH / 2];  // gate/up scales and biases of the 16 rows (bf16 pairs)
     float cw[FM_MAX_SLOTS];       // combine: every slot's weight
+    float sw;                     // combine: the shared expert's sigmoid gate
     uint32_t cvalid;              // combine: bit k = slot k is valid
     uint32_t sync;                // the item's 4-wave barrier counter
 };
@@ -724,7 +725,7 @@ struct __attribute__((aligned(16))) FmcLds {
 // only the order of the weighted sum differs from cpu_topk's slots, a
 // rounding-level difference); returns 1 / sum of the selected probabilities,
 // the renormalisation factor (computed by every wave alike).
-FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
+FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq, uint32_t etab) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int E = a.route_E, K = a.K, nch = (E + 63) >> 6;
     constexpr int NW = FMC_THREADS / 64;
@@ -739,7 +740,9 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq) {
     float lg = lgq[0];
 #pragma unroll
     for (int q = 1; q < NW; q++) lg = wv == q ? lgq[q] : lg;
-    const float ev = tid < E ? fm_expf_ref(lg - mx) : 0.f;  // the reference libm's exp, bit for bit
+    // the reference libm's exp, bit for bit (every lane active: fm_expf_lanes)
+    const float ex = fm_expf_lanes(lg - mx, etab);
+    const float ev = tid < E ? ex : 0.f;
     const float ws = fm_lane_sum<64>(ev);
     if (lane == 0) R.red[wv] = ws;
     // candidates on e = exp(l - max), before the sum is known: p = e * (1 /
@@ -923,7 +926,9 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     const uint32_t ep_ld = fm_epoch_load(a);
     constexpr bool fused = RT;
     float lgq[FMC_THREADS / 64];
+    uint32_t etab = 0;  // exp table in lanes (fm_expf_lanes), loaded with the logits
     if constexpr (RT) {
+        etab = fm_expf_lanes_load();
 #pragma unroll
         for (int q = 0; q < FMC_THREADS / 64; q++)
             lgq[q] = 64 * q + lane < a.route_E ? a.route_logits[64 * q + lane] : -INFINITY;
@@ -935,7 +940,32 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
 #pragma unroll
     for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (gt < (int)GH * 4 ? gt : 0) + 4 * j);
     float winv = 1.f;
-    if constexpr (RT) winv = fmc_route(a, L, lgq);
+    if constexpr (RT) winv = fmc_route(a, L, lgq, etab);
+    if (fused && blockIdx.x == gridDim.x - 1 && grp == FMC_NG - 1 && wv == 0) {
+        // the idle wave group of the last CU, right after the routing (the
+        // launch guarantees it holds no item, so its CU makes no down-row
+        // copy over the routing scratch):
+        // cpu_topk's slot order by serial replay, then cpu_normalize_weights
+        // (sequential sum over the slots) -- bit-equal to fm_route_kernel
+        // (issue priority raised: the replay is a long dependent chain that
+        // would otherwise queue behind the MFMA waves sharing its SIMD)
+        __builtin_amdgcn_s_setprio(3);
+        // p with cpu_softmax's sum (index order), bit-equal to the reference:
+        // scaled inside the replay unless the prologue already wrote p
+        const float pinv = L.rt.pconv ? 0.f : 1.0f / fm_serial_sum((const float *)L.rt.pb, a.route_E);
+        FM_DX_MARK(13);
+        fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt, pinv);
+        FM_DX_MARK(14);
+        __builtin_amdgcn_s_setprio(0);
+        fm_wave_lds_sync();
+        if (lane < a.K) {
+            float sm = 0.f;
+            for (int kk = 0; kk < a.K; kk++) sm += L.rt.s_val[kk];
+            const float v = L.rt.s_val[lane];
+            a.route_idx[lane] = L.rt.s_id[lane];
+            a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
+        }
+    }
     const int *rsel = RT ? L.rsel : nullptr;
     const FmSlot s = fmc_slot(a, k, rsel, L.rp, winv);
     const bool doA = has && s.valid;
@@ -985,6 +1015,11 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
             }
         }
         if (lane == 0) L.it[grp].cvalid = vm;
+        // the shared expert's gate, off the combine's critical path
+        const float swv = (a.has_shared || a.shared_y)
+                              ? (a.shared_score ? fm_sigmoid(a.shared_score[0]) : a.shared_w_host)
+                              : 0.f;
+        if (lane == 0) L.it[grp].sw = swv;
     }
     // item 0 turns x into MFMA operand rows (both layouts), group sums and
     // scales; the other items wait for them on an LDS flag, not a barrier
@@ -1224,9 +1259,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
                     if ((uint32_t)(t[kk] >> 32) != ep) t[kk] = fm_get_tagged(&a.y2[(size_t)kk * H + row]);
             } while (++it < FM_SPIN_MAX);
             if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
-            const float sw = (a.has_shared || a.shared_y)
-                                 ? (a.shared_score ? fm_sigmoid(a.shared_score[0]) : a.shared_w_host)
-                                 : 0.f;
+            const float sw = T.sw;
             const float yl = T.ylast[lane];
             float moe = 0.f;
 #pragma unroll
@@ -1267,29 +1300,6 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     if (a.pool_mode && !fused && blockIdx.x == 0 && tid < a.K) {
         const int e = a.idx[tid];
         if (e < 0 || (uint32_t)e >= a.pool_n) atomicOr(a.err, FM_STATUS_BAD_EXPERT);  // skipped (invalid slot)
-    }
-    if (fused && blockIdx.x == gridDim.x - 1 && grp == FMC_NG - 1 && wv == 0) {
-        // the idle wave group of the last CU (the launch guarantees it holds
-        // no item, so its CU makes no down-row copy over the routing scratch):
-        // cpu_topk's slot order by serial replay, then cpu_normalize_weights
-        // (sequential sum over the slots) -- bit-equal to fm_route_kernel
-        if (!L.rt.pconv) {
-            // p with cpu_softmax's sum (index order): bit-equal to the reference
-            const float pinv = 1.0f / fm_serial_sum((const float *)L.rt.pb, a.route_E);
-            fm_wave_lds_sync();
-            for (int i = lane; i < a.route_E; i += 64)
-                L.rt.pb[i] = __float_as_int(__int_as_float(L.rt.pb[i]) * pinv);
-            fm_wave_lds_sync();
-        }
-        fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt);
-        fm_wave_lds_sync();
-        if (lane < a.K) {
-            float sm = 0.f;
-            for (int kk = 0; kk < a.K; kk++) sm += L.rt.s_val[kk];
-            const float v = L.rt.s_val[lane];
-            a.route_idx[lane] = L.rt.s_id[lane];
-            a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
-        }
     }
     // Publishing the next epoch.  With the last slot valid, the combining
     // item of tile 0 has, through its waits, observed every tag user: each

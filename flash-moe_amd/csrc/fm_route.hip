@@ -82,6 +82,7 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
     FM_RT_MARK(0);
 
     // softmax: max, exp(x - max), sum, scale by 1/sum (cpu_kernels.h:263-277)
+    const uint32_t etab = fm_expf_lanes_load();  // exp table in lanes, loaded with the logits
     float v[FM_RT_VPT];
     float mx = -INFINITY;
 #pragma unroll
@@ -107,7 +108,8 @@ __global__ __launch_bounds__(FM_RT_THREADS) void fm_route_kernel(const float *__
 #pragma unroll
     for (int q = 0; q < FM_RT_VPT; q++) {
         const int i = tid + q * FM_RT_THREADS;
-        v[q] = i < E ? fm_expf_ref(v[q] - mx) : 0.f;
+        const float ex = fm_expf_lanes(v[q] - mx, etab);  // every lane active
+        v[q] = i < E ? ex : 0.f;
         if (i < E) pb[i] = __float_as_int(v[q]);
     }
     __syncthreads();

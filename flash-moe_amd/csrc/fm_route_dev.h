@@ -15,21 +15,39 @@
 
 // cpu_softmax's sum (cpu_kernels.h:269-273): v[0] + v[1] + ... in index
 // order, one rounding per term, so the sum -- and 1 / sum -- are bit-equal to
-// the reference's.  Run by one wavefront (every lane alike: the LDS reads are
-// broadcasts); v is 16-byte aligned.  ~4 cycles per term.
+// the reference's.  One wavefront, every lane active; v (LDS, 16-byte
+// aligned) holds n >= 1 floats >= 0.  Blocks of 512: lane l holds terms
+// 8l .. 8l + 7 in registers, and the running sum walks the lanes -- lane l
+// adds its 8 terms to what lane l - 1 handed it (DPP wave_shr:1), so the
+// chain is 9 VALU operations per 8 terms with no memory access in it.
+// Terms past n are +0, which leave a sum >= +0 unchanged.  Returns the sum in
+// every lane.
 FM_DEV float fm_serial_sum(const float *v, int n) {
-    float s = 0.f;
-    int i = 0;
-#pragma unroll 4
-    for (; i + 4 <= n; i += 4) {
-        const fm_f4 q = *(const fm_f4 *)(v + i);
-        s = __fadd_rn(s, q.x);
-        s = __fadd_rn(s, q.y);
-        s = __fadd_rn(s, q.z);
-        s = __fadd_rn(s, q.w);
+    const int lane = threadIdx.x & 63;
+    float carry = 0.f;
+    for (int b = 0; b < n; b += 512) {
+        float r[8];
+        const int i0 = b + 8 * lane;
+        if (i0 + 8 <= n) {
+            const fm_f4 lo = *(const fm_f4 *)(v + i0), hi = *(const fm_f4 *)(v + i0 + 4);
+            r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+            r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) r[j] = i0 + j < n ? v[i0 + j] : 0.f;
+        }
+        float s = lane == 0 ? carry : 0.f;
+        float t = s;
+        for (int l = 0; l < 64; l++) {
+            t = s;
+#pragma unroll
+            for (int j = 0; j < 8; j++) t = __fadd_rn(t, r[j]);
+            // lane l + 1 continues from lane l's sum
+            s = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x138, 0xF, 0xF, false));
+        }
+        carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 63));
     }
-    for (; i < n; i++) s = __fadd_rn(s, v[i]);
-    return s;
+    return carry;
 }
 
 FM_DEV float fm_wave_max(float v) {
@@ -107,8 +125,10 @@ FM_DEV void fm_wave_lds_sync() {
 // Serial replay on one wavefront (fallback): exact for ties.  The K slot keys
 // are kept sorted across lanes (lane 0 = the minimum, lowest slot first among
 // equal values); an insertion shifts the smaller keys down one lane.
+// pscale != 0: pb holds exp bits and the probabilities are exp * pscale
+// (scaled on the fly, pb is not written).
 template <class LDS>
-__device__ void fm_topk_serial(const int *pb, int E, int K, LDS &L) {
+__device__ void fm_topk_serial(const int *pb, int E, int K, LDS &L, float pscale = 0.f) {
     const int lane = threadIdx.x & 63;
     int kval = lane < K ? -1 : 0x7fffffff;
     int kslot = lane < K ? lane : 64;
@@ -116,7 +136,8 @@ __device__ void fm_topk_serial(const int *pb, int E, int K, LDS &L) {
     int thr = -1;
     for (int base = 0; base < E; base += 64) {
         const int i = base + lane;
-        const int p = i < E ? pb[i] : -2;
+        int p = i < E ? pb[i] : -2;
+        if (pscale != 0.f && p >= 0) p = __float_as_int(__int_as_float(p) * pscale);
         uint64_t cand = __ballot(p > thr);
         while (cand) {
             const int j = __builtin_ctzll(cand);
