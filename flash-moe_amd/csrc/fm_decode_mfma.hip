@@ -1356,9 +1356,11 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
     const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
     const bool mine = wv < a.S;
-    // one slot: wave 0 takes the gate rows, wave 1 the up rows, waves 2 and 3
-    // half of the down rows' inputs each, and the four waves share the
-    // activation polls and operand rows
+    // one slot (reached only with FMOE_DECODE_NO_SOLO set; fm_decode_solo_kernel
+    // runs one slot otherwise): waves 0 and 1 take half of the gate rows' input
+    // groups each, waves 2 and 3 half of the up rows', then waves 2 and 3 half
+    // of the down rows' inputs each; the four waves share the activation polls
+    // and operand rows
     const bool solo = a.S == 1;
     FM_DX_MARK(0);
     const uint32_t ep_ld = fm_epoch_load(a);

@@ -140,14 +140,21 @@ def test_moe_decode_valid_mask_and_no_shared(orc, dev):
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("solo", [True, False])
 @pytest.mark.parametrize("bits", [4, 2])
-def test_moe_decode_single_expert(orc, dev, bits):
-    """Config 1: one expert x router weight, no shared expert (one slot: the
-    few-slot kernel's single-slot path, where every workgroup adds the gate/up
-    partials of all tiles itself).  Three calls on one workspace, new inputs
-    each time, plus the per-expert output mode (encode_experts_batched)."""
+def test_moe_decode_single_expert(orc, dev, bits, solo, monkeypatch):
+    """Config 1: one expert x router weight, no shared expert.  One slot runs
+    on fm_decode_solo_kernel (each workgroup computes whole gate/up rows, one
+    hand-off); with FMOE_DECODE_NO_SOLO=1 on the few-slot kernel's one-slot
+    path (gate and up rows split over the waves).  Three calls on one
+    workspace, new inputs each time, plus the per-expert output mode
+    (encode_experts_batched)."""
     import torch
-    say("moe_decode single expert", bits)
+    if solo:
+        monkeypatch.delenv("FMOE_DECODE_NO_SOLO", raising=False)
+    else:
+        monkeypatch.setenv("FMOE_DECODE_NO_SOLO", "1")
+    say("moe_decode single expert", bits, "solo" if solo else "few-slot kernel")
     ws = fm.workspace(fm.decode_workspace_bytes(1, HIDDEN, INTER), dev)
     out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
     ob = torch.empty(HIDDEN, dtype=torch.int16, device=dev)
