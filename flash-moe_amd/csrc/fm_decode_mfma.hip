@@ -259,6 +259,61 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
     }
 }
 
+// fmm_mma<4, NG> with the x operand read from LDS: lanes whose row m carries
+// the group of a block of 4 steps read their own 4 operand quads, the others
+// a zero run (one address select per block instead of 4 v_cndmask a step; the
+// next block's quads are read while the current block's MFMAs run).  For one
+// wave alone (the last item's down rows, on the step's critical path) this
+// measured 29 ns a step against 36 ns.  `zero` must hold 16 zero pairs.
+template <int NG = 16>
+FM_DEV void fmm_mma_l4(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, uint32_t *T, fmm_f4 &d0,
+                       fmm_f4 &d1, int lane) {
+    const int m = lane & 15, kq = lane >> 4;
+    const bool kq_on = (kq >> 1) == (m & 1);
+    const fm_h2 *own = xq_grp0 + 32 * m + 16 * (kq & 1);
+    auto blk_src = [&](int blk) -> const fm_h2 * {
+        const int c = blk >> 1, h = blk & 1;
+        return (kq_on && c == (m >> 2) && h == ((m >> 1) & 1)) ? own : zero;
+    };
+    constexpr int NB = NG / 2;  // blocks of 4 steps
+    fmm_h8 xa[4], xb[4];
+    {
+        const fm_h2 *sp = blk_src(0);
+#pragma unroll
+        for (int s = 0; s < 4; s++) xa[s] = fmm_lds_op(sp + 4 * s);
+    }
+#pragma unroll
+    for (int p = 0; p < NG / 8; p++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(fm_u4 *)&T[(4 * j + kq) * FMM_TS + 4 * m] = cd.c[4 * p + j];
+        fm_u4 v[4];
+#pragma unroll
+        for (int h = 0; h < 4; h++) v[h] = *(const fm_u4 *)&T[m * FMM_TS + 16 * h + 4 * kq];
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            const int blk = 4 * p + bb;
+            if (blk + 1 < NB) {
+                const fm_h2 *sp = blk_src(blk + 1);
+#pragma unroll
+                for (int s = 0; s < 4; s++) xb[s] = fmm_lds_op(sp + 4 * s);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int j = 4 * blk + s;
+                const int c = j >> 3, i = j & 7;
+                const fmm_h8 co = fmm_codes<4>(fmm_comp(v[2 * (c & 1) + (i >> 2)], i & 3), 0);
+                if (i & 1)
+                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s], co, d1, 0, 0, 0);
+                else
+                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s], co, d0, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; s++) xa[s] = xb[s];
+        }
+    }
+}
+
 
 // A slot descriptor read from LDS is the same in every lane: keep it in scalar registers.
 FM_DEV FmSlot fmm_uniform(const FmSlot &v) {
@@ -1215,7 +1270,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &T.aq[s.bits == 4 ? 0 : 1][0][0];
         if (s.bits == 4)
-            fmm_mma<4, NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+            fmm_mma_l4<NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
         else
             fmm_mma<2, NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
         const bool qok = 4 * q < NG;
