@@ -111,7 +111,7 @@ struct FmmCodes {
 // piece (4 loads) and a 2-bit one half a piece (lanes n >= 8 repeat lane n - 8).
 template <int NG = 16>
 FM_DEV void fmm_issue_codes(const uint32_t *W, int bits, uint32_t row0, uint32_t in_dim, uint32_t g0, bool ok,
-                            FmmCodes &cd, int lane, const void *dummy) {
+                            FmmCodes &cd, int lane, const void *dummy, int pmask = 3) {
     const int n = lane & 15, kq = lane >> 4;
     const uint32_t G = in_dim / 64, wpg = 2 * bits, wpr = ok ? G * wpg : 0;
     if (!ok) {
@@ -128,7 +128,9 @@ FM_DEV void fmm_issue_codes(const uint32_t *W, int bits, uint32_t row0, uint32_t
         for (int j = 0; j < 4; j++) {
             const uint32_t row = row0 + 4 * j + kq;
             const uint32_t po = (ok && bits == 4) ? g0 * wpg + 64 * p : (ok ? g0 * wpg : 0);
-            cd.c[4 * p + j] = fm_ldg_u4_nt(W + (size_t)row * wpr + po + 4 * nw);
+            // pieces outside pmask read the dummy (same load count, cache hits)
+            cd.c[4 * p + j] = fm_ldg_u4_nt(((pmask >> p) & 1) ? W + (size_t)row * wpr + po + 4 * nw
+                                                               : (const uint32_t *)dummy);
         }
     }
 }
@@ -265,7 +267,8 @@ FM_DEV void fmm_mma(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero,
 // next block's quads are read while the current block's MFMAs run).  For one
 // wave alone (the last item's down rows, on the step's critical path) this
 // measured 29 ns a step against 36 ns.  `zero` must hold 16 zero pairs.
-template <int NG = 16>
+// P0 .. P1 - 1: the pieces (8 groups each) computed.
+template <int NG = 16, int P0 = 0, int P1 = NG / 8>
 FM_DEV void fmm_mma_l4(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *zero, uint32_t *T, fmm_f4 &d0,
                        fmm_f4 &d1, int lane) {
     const int m = lane & 15, kq = lane >> 4;
@@ -275,15 +278,15 @@ FM_DEV void fmm_mma_l4(const FmmCodes &cd, const fm_h2 *xq_grp0, const fm_h2 *ze
         const int c = blk >> 1, h = blk & 1;
         return (kq_on && c == (m >> 2) && h == ((m >> 1) & 1)) ? own : zero;
     };
-    constexpr int NB = NG / 2;  // blocks of 4 steps
+    constexpr int NB = 4 * P1;  // blocks of 4 steps
     fmm_h8 xa[4], xb[4];
     {
-        const fm_h2 *sp = blk_src(0);
+        const fm_h2 *sp = blk_src(4 * P0);
 #pragma unroll
         for (int s = 0; s < 4; s++) xa[s] = fmm_lds_op(sp + 4 * s);
     }
 #pragma unroll
-    for (int p = 0; p < NG / 8; p++) {
+    for (int p = P0; p < P1; p++) {
 #pragma unroll
         for (int j = 0; j < 4; j++) *(fm_u4 *)&T[(4 * j + kq) * FMM_TS + 4 * m] = cd.c[4 * p + j];
         fm_u4 v[4];
@@ -721,6 +724,10 @@ struct __attribute__((aligned(16))) FmcItem {
     uint32_t sync;                // the item's 4-wave barrier counter
 };
 
+#ifndef FMC_DN_HELP
+#define FMC_DN_HELP 1  // item 0's waves take half of the last item's down MMA (see fm_decode_cu_kernel)
+#endif
+
 #ifndef FMC_DN_LDS
 #define FMC_DN_LDS 1  // the last item's down rows copied into LDS early (see fm_decode_cu_kernel)
 #endif
@@ -745,6 +752,9 @@ struct __attribute__((aligned(16))) FmcLds {
     float xinv[FMM_GH];
     uint32_t xready;              // count of item 0's waves that built the x operands
     uint32_t dn_ready;            // count of item 0's waves whose copy of the last item's down rows landed
+    uint32_t hlp_go;              // the last item's activation operands are built (its helpers may start)
+    uint32_t hlp_done[4];         // helper wave w has written hy[w]
+    float hy[4][16];              // helper wave w: groups 8..15 of the last item's wave-w down rows
     FmcItem it[FMC_NG];
     union {
         // the routing scratch is dead once every wave has passed the
@@ -970,8 +980,9 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     FM_DX_MARK(0);
     // counters first (no load is in flight yet, so this barrier is cheap)
     if (tid < FMC_NG) L.it[tid].sync = 0;
+    if (tid < 4) L.hlp_done[tid] = 0;
     if (tid == 0) {
-        L.xready = L.dn_ready = 0;
+        L.xready = L.dn_ready = L.hlp_go = 0;
         if constexpr (RT) {
             L.rt.ncand = L.rt.pconv = 0;  // fused routing: candidate count, p written into pb
             L.rt.vk = -1;                 // ... and the first probability left out (none)
@@ -1033,7 +1044,15 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // (the 8-group instance only: with the combining slot on the two-item CUs
     // the 16-group step measured 0.2 us faster without the copy)
     constexpr bool DNL = FMC_DN_LDS && NG == 8;
-    const FmSlot s_l = (DNL && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv) : s;
+    // The last item's down MMA (on the step's critical path: its activations
+    // arrive last) is split with item 0's waves, idle by then: item 0's wave w
+    // computes groups 8..15 of the last item's wave-w rows from codes it loads
+    // right after its own down rows, and hands the partial sums over in LDS.
+    // Only for 4-bit slots (one wave per SIMD becomes two).
+    constexpr bool HLP = FMC_DN_HELP && NG == 16;
+    const FmSlot s_l = ((DNL || HLP) && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv) : s;
+    const bool help0 = HLP && grp == 0 && has_l && s_l.valid && s_l.bits == 4;
+    const bool help2 = HLP && grp == FMC_NG - 1 && doA && s.bits == 4;
     const bool dn_lds = DNL && (grp == 0 ? has_l && s_l.valid : (grp == FMC_NG - 1 && doA));
     // Every gate/up load of the item.  Loads issue in order and block while
     // the CU's request queue is full, so a wave issues its down rows only
@@ -1191,8 +1210,16 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // item's come from LDS (its loads read the dummy, so the count of loads in
     // flight is the same on every path)
     const bool dn_glob = doA && !(dn_lds && grp == FMC_NG - 1);
-    fmm_issue_codes<NG>(s.dw, bits, rowB0, I, 0, dn_glob, cdn, lane, a.x);
+    fmm_issue_codes<NG>(s.dw, bits, rowB0, I, 0, dn_glob, cdn, lane, a.x, help2 ? 1 : 3);
     fmm_issue_sb<NG>(s.ds, s.db, rowB0, I, 0, dn_glob, sdn, bdn, lane, a.x);
+    // item 0's share of the last item's down rows (piece 1: groups 8..15)
+    FmmCodes chl;
+    fmm_u2 sdh = {0, 0}, bdh = {0, 0};
+    if constexpr (HLP) {
+        const uint32_t rowBl = (item_l % TILES) * 64 + 16 * wv;
+        fmm_issue_codes<NG>(s_l.dw, 4, rowBl, I, 0, help0, chl, lane, a.x, 2);
+        fmm_issue_sb<NG>(s_l.ds, s_l.db, rowBl, I, 0, help0, sdh, bdh, lane, a.x);
+    }
     if (dn_lds && grp == 0) {
         // the copy is older than the NG / 2 + 2 loads just issued
         static_assert(NG / 2 + 2 <= 15, "vmcnt immediate");
@@ -1243,6 +1270,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     }
     fmc_item_sync(&T.sync, phase);
     FM_DX_MARK(5);
+    if (help2 && wv == 0 && lane == 0) __hip_atomic_fetch_add(&L.hlp_go, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (dn_lds && grp == FMC_NG - 1) {
         // this item's down rows from LDS, in the lane layout of fmm_issue_codes / fmm_issue_sb
         uint32_t it = 0;
@@ -1269,13 +1297,24 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     if (doA) {
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &T.aq[s.bits == 4 ? 0 : 1][0][0];
-        if (s.bits == 4)
+        if (help2)
+            fmm_mma_l4<NG, 0, 1>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
+        else if (s.bits == 4)
             fmm_mma_l4<NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
         else
             fmm_mma<2, NG>(cdn, aq, L.zero, T.tr[wv], d0, d1, lane);
-        const bool qok = 4 * q < NG;
+        const bool qok = 4 * q < NG && !(help2 && q >= 2);
         float y = qok ? fmm_fold(d0 + d1, sdn, bdn, &T.asum[4 * (qok ? q : 0)], &T.ainv[4 * (qok ? q : 0)]) : 0.f;
-        y = fmm_q_sum(y);
+        y = fmm_q_sum(y);  // with the helper: (q0 + q1) here, (q2 + q3) from it -- the same sum
+        if (help2) {
+            uint32_t it = 0;
+            while (__hip_atomic_load(&L.hlp_done[wv], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0 &&
+                   ++it < FM_SPIN_MAX)
+                __builtin_amdgcn_s_sleep(1);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+            asm volatile("" ::: "memory");
+            y += L.hy[wv][n];
+        }
         const uint32_t row = rowB0 + n;
         if (lane < 16) {
             if (a.mode == 1)
@@ -1350,6 +1389,24 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
                 a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
             }
         }
+    }
+    if (help0) {
+        // item 0's wave wv: groups 8..15 of the last item's wave-wv down rows,
+        // once that item's activation operands are built
+        uint32_t it = 0;
+        while (__hip_atomic_load(&L.hlp_go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0 && ++it < FM_SPIN_MAX)
+            __builtin_amdgcn_s_sleep(1);
+        if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+        asm volatile("" ::: "memory");
+        FmcItem &T2 = L.it[FMC_NG - 1];
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        fmm_mma_l4<NG, 1, 2>(chl, &T2.aq[0][0][0], L.zero, T.tr[wv], d0, d1, lane);
+        const int qh = q >= 2 ? q : 2;
+        float yh = q >= 2 ? fmm_fold(d0 + d1, sdh, bdh, &T2.asum[4 * qh], &T2.ainv[4 * qh]) : 0.f;
+        yh = fmm_q_sum(yh);
+        if (lane < 16) L.hy[wv][n] = yh;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): hy is written
+        if (lane == 0) __hip_atomic_fetch_add(&L.hlp_done[wv], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     FM_DX_MARK(7);
     if (a.pool_mode && !fused && blockIdx.x == 0 && tid < a.K) {
