@@ -498,8 +498,8 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[sA.bits == 4 ? 0 : 1][16 * wv][0];
         if (sA.bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            fmm_mma_l4(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma_l4(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         } else {
             fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
             fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
@@ -600,7 +600,7 @@ __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfm
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *aq = &L.aq[sB.bits == 4 ? 0 : 1][0][0];
         if (sB.bits == 4)
-            fmm_mma<4>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma_l4(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         else
             fmm_mma<2>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         float y = fmm_fold(d0 + d1, sdn, bdn, &L.asum[4 * q], &L.ainv[4 * q]);
@@ -1561,7 +1561,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][8 * h][0];
         if (bits == 4)
-            fmm_mma<4, 8>(wv < 2 ? cg : cu, xq, L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma_l4<8>(wv < 2 ? cg : cu, xq, L.zero, L.tr[wv], d0, d1, lane);
         else
             fmm_mma<2, 8>(wv < 2 ? cg : cu, xq, L.zero, L.tr[wv], d0, d1, lane);
         FM_DX_MARK(2);
@@ -1578,8 +1578,8 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][0][0];
         if (bits == 4) {
-            fmm_mma<4>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
-            fmm_mma<4>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
+            fmm_mma_l4(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
+            fmm_mma_l4(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
         } else {
             fmm_mma<2>(cg, xq, L.zero, L.tr[wv], g0, g1, lane);
             fmm_mma<2>(cu, xq, L.zero, L.tr[wv], u0, u1, lane);
@@ -1713,7 +1713,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
             const int h = wv & 1;
             const fm_h2 *aq = &L.aq[0][bits == 4 ? 0 : 1][8 * h][0];
             if (bits == 4)
-                fmm_mma<4, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
+                fmm_mma_l4<8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
             else
                 fmm_mma<2, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
             const bool qok = q < 2;
@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
             y = fmm_q_sum(qok ? fmm_fold(d0 + d1, sdn, bdn, &L.asum[0][gq], &L.ainv[0][gq]) : 0.f);
         } else {
             if (bits == 4)
-                fmm_mma<4>(cdn, &L.aq[ys][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
+                fmm_mma_l4(cdn, &L.aq[ys][0][0][0], L.zero, L.tr[wv], d0, d1, lane);
             else
                 fmm_mma<2>(cdn, &L.aq[ys][1][0][0], L.zero, L.tr[wv], d0, d1, lane);
             y = fmm_q_sum(fmm_fold(d0 + d1, sdn, bdn, &L.asum[ys][4 * q], &L.ainv[ys][4 * q]));
@@ -1892,7 +1892,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
         const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][16 * wv][0];
         if (bits == 4)
-            fmm_mma<4>(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma_l4(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
         else
             fmm_mma<2>(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
         const float ph = fmm_q_sum(fmm_fold(d0 + d1, sc, bi, &L.xsum[16 * wv + 4 * q], &L.xinv[16 * wv + 4 * q]));
@@ -1953,7 +1953,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
         const int h = wv & 1;
         const fm_h2 *aq = &L.aq[8 * h][0];
         if (bits == 4)
-            fmm_mma<4, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma_l4<8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         else
             fmm_mma<2, 8>(cdn, aq, L.zero, L.tr[wv], d0, d1, lane);
         const bool qok = q < 2;
