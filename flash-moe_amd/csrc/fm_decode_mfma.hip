@@ -1779,13 +1779,16 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
 // ------------------------------------------------ one slot (config 1) ----
 // One expert (or the shared expert alone) with a single cross-workgroup
 // hand-off: workgroup g computes gate and up rows 4g .. 4g + 3 over all 4096
-// inputs (wave w: input quarter w; the 16 MFMA columns are the 4 gate rows,
-// the 4 up rows and 8 zero columns), adds the quarters in LDS in the order
-// (q0 + q1) + (q2 + q3) and publishes its 4 activations; every workgroup then
-// polls the 1024 activations and computes down rows 16g .. 16g + 15 (waves 2
-// and 3, half of the inputs each) and the combine of those rows.  (The
+// inputs (wave w of 8: input eighth w, 16 MMA steps; the 16 MFMA columns are
+// the 4 gate rows, the 4 up rows and 8 zero columns), adds the eighths in LDS
+// in the order ((e0 + e1) + (e2 + e3)) + ((e4 + e5) + (e6 + e7)) and publishes
+// its 4 activations; every workgroup then polls the 1024 activations and
+// computes down rows 16g .. 16g + 15 (waves 6 and 7, half of the inputs each)
+// and the combine of those rows.  Eight waves rather than four: one wave's MMA
+// steps form a latency chain, and two waves on a SIMD overlap theirs.  (The
 // few-slot kernel below hands quarter partials to a reducing workgroup
 // first: one more round trip.)
+#define FMO_W 8  // waves of the one-slot kernel: one input eighth each in the gate/up MMA
 struct __attribute__((aligned(16))) FmoLds {
     fm_h2 xq[2][FMM_GH][32];  // x as operand rows (4-bit | 2-bit layout)
     float xsum[FMM_GH], xinv[FMM_GH];
@@ -1793,12 +1796,12 @@ struct __attribute__((aligned(16))) FmoLds {
     fm_h2 aq[FMM_GI][32];     // the activations as operand rows (the slot's layout)
     float asum[FMM_GI], ainv[FMM_GI];
     float act[FMM_MAXI];
-    float ph[4][8];           // per wave (input quarter): partials of the 4 gate and 4 up rows
+    float ph[FMO_W][8];       // per wave (input eighth): partials of the 4 gate and 4 up rows
     float pu[16];             // the second half of the down rows
-    uint32_t tr[4][16 * FMM_TS];
+    uint32_t tr[FMO_W][16 * FMM_TS];
 };
 
-__global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) {
+__global__ __launch_bounds__(64 * FMO_W, 1) void fm_decode_solo_kernel(FmDecodeArgs a) {
     __shared__ FmoLds L;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1807,31 +1810,33 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
     const uint32_t g = blockIdx.x, rowA0 = 4 * g, rowB0 = 16 * g;
     FM_DX_MARK(0);
     const uint32_t ep_ld = fm_epoch_load(a);
-    // x: thread t holds elements 16 t .. 16 t + 15 (group t / 4)
+    // x: thread t < 256 holds elements 16 t .. 16 t + 15 (group t / 4)
     fm_f4 xr[4];
+    const bool xt = tid < 256;
 #pragma unroll
-    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * tid + 4 * j);
+    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (xt ? tid : 0) + 4 * j);
     const FmSlot s = fmc_slot(a, 0);
     const bool ok = s.valid;
     const int bits = ok ? s.bits : 4;
-    // gate / up codes of input quarter wv: MFMA column 4j + kq is gate row
-    // rowA0 + kq (j = 0) or up row rowA0 + kq (j = 1); columns 8..15 are zero
+    // gate / up codes of input eighth wv (8 groups: one 4-bit piece, half a
+    // 2-bit one, whose lanes n >= 8 repeat lane n - 8): MFMA column 4j + kq is
+    // gate row rowA0 + kq (j = 0) or up row rowA0 + kq (j = 1); columns 8..15
+    // are zero
     FmmCodes cd;
     fmm_u2 sc = {0u, 0u}, bi = {0u, 0u};
     {
-        const uint32_t wpg = 2 * bits, wpr = (H / 64) * wpg, g0 = 16 * wv;
+        const uint32_t wpg = 2 * bits, wpr = (H / 64) * wpg, g0 = 8 * wv;
         const uint32_t *gw = ok ? s.gw : (const uint32_t *)a.x, *uw = ok ? s.uw : (const uint32_t *)a.x;
         const uint32_t row = ok ? rowA0 + q : 0;
         const uint32_t rw = ok ? wpr : 0;
+        const int nw = bits == 2 ? (n & 7) : n;
+        const uint32_t po = ok ? g0 * wpg : 0;
+        cd.c[0] = fm_ldg_u4_nt(gw + (size_t)row * rw + po + 4 * nw);
+        cd.c[1] = fm_ldg_u4_nt(uw + (size_t)row * rw + po + 4 * nw);
 #pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const uint32_t po = ok ? g0 * wpg + (bits == 4 ? 64 * p : 0) : 0;
-            cd.c[4 * p + 0] = fm_ldg_u4_nt(gw + (size_t)row * rw + po + 4 * n);
-            cd.c[4 * p + 1] = fm_ldg_u4_nt(uw + (size_t)row * rw + po + 4 * n);
-            cd.c[4 * p + 2] = cd.c[4 * p + 3] = (fm_u4){0u, 0u, 0u, 0u};
-        }
-        // scale / bias runs: lane (n, q) = column n, groups g0 + 4q .. + 3
-        const bool mine = ok && n < 8;
+        for (int j = 2; j < 8; j++) cd.c[j] = (fm_u4){0u, 0u, 0u, 0u};
+        // scale / bias runs: lane (n, q) = column n, groups g0 + 4q .. + 3 (q < 2)
+        const bool mine = ok && n < 8 && q < 2;
         const uint16_t *S_ = n < 4 ? s.gs : s.us, *B_ = n < 4 ? s.gb : s.ub;
         const size_t o = mine ? (size_t)(rowA0 + (n & 3)) * (H / 64) + g0 + 4 * q : 0;
         const fmm_u2 sv = *(const FM_GLOBAL fmm_u2 *)(mine ? S_ + o : (const uint16_t *)a.x);
@@ -1839,13 +1844,13 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
         sc = mine ? sv : (fmm_u2){0u, 0u};
         bi = mine ? bv : (fmm_u2){0u, 0u};
     }
-    // down rows rowB0 .. + 15: waves 2, 3 take input groups 0-7, 8-15
-    const bool doD = ok && wv >= 2;
+    // down rows rowB0 .. + 15: waves 6, 7 take input groups 0-7, 8-15
+    const bool doD = ok && wv >= FMO_W - 2;
     FmmCodes cdn;
     fmm_u2 sdn, bdn;
     fmm_issue_codes<8>(s.dw, bits, rowB0, I, 8 * (wv & 1), doD, cdn, lane, a.x);
     fmm_issue_sb<8>(s.ds, s.db, rowB0, I, 8 * (wv & 1), doD, sdn, bdn, lane, a.x);
-    {
+    if (xt) {
         // x -> operand rows (both layouts), group sums and scales
         const int gg = tid >> 2, qq = tid & 3;
         float v[16];
@@ -1887,46 +1892,53 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
     __syncthreads();
     FM_DX_MARK(1);
     const uint32_t ep = fm_epoch_tag(ep_ld);
-    // ---- A: quarter wv of the 4 gate and 4 up rows, the quarters added in LDS ----
+    // ---- A: eighth wv of the 4 gate and 4 up rows, the eighths added in LDS ----
     if (ok) {
         fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
-        const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][16 * wv][0];
+        const fm_h2 *xq = &L.xq[bits == 4 ? 0 : 1][8 * wv][0];
         if (bits == 4)
-            fmm_mma_l4(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
+            fmm_mma_l4<8>(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
         else
-            fmm_mma<2>(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
-        const float ph = fmm_q_sum(fmm_fold(d0 + d1, sc, bi, &L.xsum[16 * wv + 4 * q], &L.xinv[16 * wv + 4 * q]));
+            fmm_mma<2, 8>(cd, xq, L.zero, L.tr[wv], d0, d1, lane);
+        const int qq = q < 2 ? q : 0;
+        const float f = q < 2 ? fmm_fold(d0 + d1, sc, bi, &L.xsum[8 * wv + 4 * qq], &L.xinv[8 * wv + 4 * qq]) : 0.f;
+        const float ph = fmm_q_sum(f);
         if (lane < 8) L.ph[wv][lane] = ph;
     }
     __syncthreads();
     FM_DX_MARK(2);
     if (ok && tid < 4) {
-        const float gs = (L.ph[0][tid] + L.ph[1][tid]) + (L.ph[2][tid] + L.ph[3][tid]);
-        const float us = (L.ph[0][4 + tid] + L.ph[1][4 + tid]) + (L.ph[2][4 + tid] + L.ph[3][4 + tid]);
+        const float gs = ((L.ph[0][tid] + L.ph[1][tid]) + (L.ph[2][tid] + L.ph[3][tid])) +
+                         ((L.ph[4][tid] + L.ph[5][tid]) + (L.ph[6][tid] + L.ph[7][tid]));
+        const float us = ((L.ph[0][4 + tid] + L.ph[1][4 + tid]) + (L.ph[2][4 + tid] + L.ph[3][4 + tid])) +
+                         ((L.ph[4][4 + tid] + L.ph[5][4 + tid]) + (L.ph[6][4 + tid] + L.ph[7][4 + tid]));
         fm_put_tagged(&a.act2[rowA0 + tid], fm_silu_mul(gs, us), ep);
     }
     FM_DX_MARK(3);
-    // ---- B: the 1024 activations (wave w polls 256 w .. + 255), operand rows ----
+    // ---- B: the 1024 activations (wave w polls its eighth), operand rows ----
     if (ok) {
-        const uint64_t *src = a.act2 + 256 * wv;
-        uint64_t t[4];
+        constexpr int PQ = FMM_MAXI / (64 * FMO_W);  // words per lane
+        const uint64_t *src = a.act2 + (FMM_MAXI / FMO_W) * wv;
+        uint64_t t[PQ];
 #pragma unroll
-        for (int j = 0; j < 4; j++) t[j] = fm_get_tagged(src + 64 * j + lane);
+        for (int j = 0; j < PQ; j++) t[j] = fm_get_tagged(src + 64 * j + lane);
         uint32_t it = 0;
         do {
             bool ready = true;
 #pragma unroll
-            for (int j = 0; j < 4; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+            for (int j = 0; j < PQ; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
             if (__all(ready)) break;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < PQ; j++)
                 if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(src + 64 * j + lane);
         } while (++it < FM_SPIN_MAX);
         if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
         FM_DX_MARK(4);
 #pragma unroll
-        for (int j = 0; j < 4; j++) L.act[256 * wv + 64 * j + lane] = __uint_as_float((uint32_t)t[j]);
+        for (int j = 0; j < PQ; j++) L.act[(FMM_MAXI / FMO_W) * wv + 64 * j + lane] = __uint_as_float((uint32_t)t[j]);
         __syncthreads();
+    }
+    if (ok && tid < 256) {
         const int lay = bits == 4 ? 0 : 1;
         const uint32_t gg = tid >> 4;
         const float *ag = &L.act[64 * gg + 4 * (tid & 15)];
@@ -1943,9 +1955,9 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
         (void)lay;
         fmm_build_pair(&L.act[64 * gg], bits, 2 * (tid & 15), f, &L.aq[gg][0]);
         fmm_build_pair(&L.act[64 * gg], bits, 2 * (tid & 15) + 1, f, &L.aq[gg][0]);
-        __syncthreads();
     }
-    // ---- C: down rows rowB0 .. + 15 (waves 2, 3: halves of the inputs), combine ----
+    if (ok) __syncthreads();
+    // ---- C: down rows rowB0 .. + 15 (waves 6, 7: halves of the inputs), combine ----
     float y = 0.f;
     if (doD) {
         FM_DX_MARK(5);
@@ -1959,14 +1971,14 @@ __global__ __launch_bounds__(256, 1) void fm_decode_solo_kernel(FmDecodeArgs a) 
         const bool qok = q < 2;
         const int gq = 8 * h + 4 * (qok ? q : 0);
         y = fmm_q_sum(qok ? fmm_fold(d0 + d1, sdn, bdn, &L.asum[gq], &L.ainv[gq]) : 0.f);
-        if (wv == 3 && lane < 16) L.pu[n] = y;
+        if (wv == FMO_W - 1 && lane < 16) L.pu[n] = y;
     }
     __syncthreads();
     FM_DX_MARK(6);
     // every workgroup waited for all 1024 activations, each published after
     // its workgroup's four waves read the epoch: one plain store publishes it
     if (g == 0 && tid == 0) fm_epoch_publish(a, ep);
-    if (wv == 2 && lane < 16) {
+    if (wv == FMO_W - 2 && lane < 16) {
         const uint32_t row = rowB0 + lane;
         if (ok) y += L.pu[n];
         if (a.mode == 1) {
@@ -2049,7 +2061,7 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
             // one slot: one hand-off (FMOE_DECODE_NO_SOLO set: the few-slot kernel, which tests compare)
             const char *no_solo = getenv("FMOE_DECODE_NO_SOLO");
             if (a.S == 1 && a.ntok <= 1 && !(no_solo && *no_solo)) {
-                hipLaunchKernelGGL(fm_decode_solo_kernel, dim3(FMS_GRID), dim3(256), 0, st, a);
+                hipLaunchKernelGGL(fm_decode_solo_kernel, dim3(FMS_GRID), dim3(64 * FMO_W), 0, st, a);
                 return fm_check_launch("fm_decode_solo_kernel");
             }
             hipLaunchKernelGGL(fm_decode_split_kernel, dim3(FMS_GRID), dim3(256), 0, st, a);
