@@ -1936,27 +1936,28 @@ __global__ __launch_bounds__(64 * FMO_W, 1) void fm_decode_solo_kernel(FmDecodeA
         FM_DX_MARK(4);
 #pragma unroll
         for (int j = 0; j < PQ; j++) L.act[(FMM_MAXI / FMO_W) * wv + 64 * j + lane] = __uint_as_float((uint32_t)t[j]);
-        __syncthreads();
-    }
-    if (ok && tid < 256) {
-        const int lay = bits == 4 ? 0 : 1;
-        const uint32_t gg = tid >> 4;
-        const float *ag = &L.act[64 * gg + 4 * (tid & 15)];
+        // this wave's two groups (its own polled activations) -> operand rows,
+        // sums and scales: lanes 0-15 group 2 wv, lanes 16-31 group 2 wv + 1
+        // (16 threads x 4 elements a group; lanes 32-63 repeat them, unused)
+        fm_wave_lds_sync();
+        const uint32_t gg = 2 * wv + ((lane >> 4) & 1), tg = lane & 15;
+        const float *ag = &L.act[64 * gg + 4 * tg];
         float sm = (ag[0] + ag[1]) + (ag[2] + ag[3]);
         float mx = fmaxf(fmaxf(fabsf(ag[0]), fabsf(ag[1])), fmaxf(fabsf(ag[2]), fabsf(ag[3])));
         sm = fmm_row_sum(sm);
         mx = fm_row16_max(mx);
         const int ex = fm_group_shift(mx);
         const float f = fm_exp2i(ex);
-        if ((tid & 15) == 0) {
-            L.asum[gg] = sm;
-            L.ainv[gg] = fm_exp2i(24 - ex);
+        if (lane < 32) {
+            if (tg == 0) {
+                L.asum[gg] = sm;
+                L.ainv[gg] = fm_exp2i(24 - ex);
+            }
+            fmm_build_pair(&L.act[64 * gg], bits, 2 * tg, f, &L.aq[gg][0]);
+            fmm_build_pair(&L.act[64 * gg], bits, 2 * tg + 1, f, &L.aq[gg][0]);
         }
-        (void)lay;
-        fmm_build_pair(&L.act[64 * gg], bits, 2 * (tid & 15), f, &L.aq[gg][0]);
-        fmm_build_pair(&L.act[64 * gg], bits, 2 * (tid & 15) + 1, f, &L.aq[gg][0]);
+        __syncthreads();
     }
-    if (ok) __syncthreads();
     // ---- C: down rows rowB0 .. + 15 (waves 6, 7: halves of the inputs), combine ----
     float y = 0.f;
     if (doD) {
