@@ -738,6 +738,7 @@ struct __attribute__((aligned(16))) FmcRoute {
     int pb[FMC_THREADS];              // exp(l - max) bits (probability bits once pconv), -2 past E
     int cv[FMC_THREADS + 4];          // top-K candidates: probability bits
     int ci[FMC_THREADS + 4];          // ... and element indices
+    uint64_t ck[FMC_THREADS / 8];     // ... and their ranking keys (e bits, then 1023 - index), zero past the count
     float red[FMC_THREADS / 64];      // per-wave sums of exp(l - max)
     float inv;                        // 1 / softmax sum (per-wave sums: the kernel's own weights)
     int ncand, ek1, vk, pconv;        // candidates; e bits at places K - 1 and K; pb holds exact p
@@ -825,49 +826,44 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq, uint3
             const int pos = base + fm_mbcnt(m);
             R.cv[pos] = eb;
             R.ci[pos] = tid;
+            if (pos < FMC_THREADS / 8) R.ck[pos] = ((uint64_t)(uint32_t)eb << 32) | (uint32_t)(1023 - tid);
         }
     }
     __syncthreads();
     FM_DX_MARK(10);
-    // the softmax sum with fm_route_kernel's arithmetic (the same per-wave
-    // sums added in wave order; waves past E add zeros), so p is bit-equal
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) sum += R.red[w];
-    const float inv = 1.0f / sum;
     const int NC = R.ncand;
     // a candidate's place = the number of candidates ahead of it by the key
     // (e bits, then the lower index first): unique places, so place K - 1 is
     // the last selected and place K the first left out
+    float inv = 0.f;
     if (NC <= FMC_THREADS / 8) {
-        // eight lanes per candidate (lane r: entries 12 r .. 12 r + 11), 64-bit
-        // keys, counts summed over the 8 lanes (quad_perm [1,0,3,2],
-        // [2,3,0,1], row_half_mirror)
+        // eight lanes per candidate (lane r: keys 12 r .. 12 r + 11, zero past
+        // the count, so no bound check), counts summed over the 8 lanes
+        // (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror)
         const int c = tid >> 3, r = tid & 7;
         const bool act = c < NC;
-        const uint64_t key = act ? ((uint64_t)(uint32_t)R.cv[c] << 32) | (uint32_t)(1023 - R.ci[c]) : 0;
+        const uint64_t key = act ? R.ck[c] : 0;
         int cnt = 0;
         if (act) {
-            int4 cv4[3], ci4[3];
+            uint64_t kk[12];
 #pragma unroll
-            for (int h = 0; h < 3; h++) {
-                cv4[h] = *reinterpret_cast<const int4 *>(&R.cv[12 * r + 4 * h]);
-                ci4[h] = *reinterpret_cast<const int4 *>(&R.ci[12 * r + 4 * h]);
+            for (int h = 0; h < 6; h++) {
+                const fm_u4 v = *reinterpret_cast<const fm_u4 *>(&R.ck[12 * r + 2 * h]);
+                kk[2 * h] = ((uint64_t)v.y << 32) | v.x;
+                kk[2 * h + 1] = ((uint64_t)v.w << 32) | v.z;
             }
 #pragma unroll
-            for (int h = 0; h < 3; h++) {
-                const int cc[4] = {cv4[h].x, cv4[h].y, cv4[h].z, cv4[h].w};
-                const int dd[4] = {ci4[h].x, ci4[h].y, ci4[h].z, ci4[h].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint64_t kj = ((uint64_t)(uint32_t)cc[q] << 32) | (uint32_t)(1023 - dd[q]);
-                    cnt += (12 * r + 4 * h + q < NC && kj > key) ? 1 : 0;
-                }
-            }
+            for (int j = 0; j < 12; j++) cnt += kk[j] > key ? 1 : 0;
         }
         cnt += fm_dpp_i<0xB1>(cnt);
         cnt += fm_dpp_i<0x4E>(cnt);
         cnt += fm_dpp_i<0x141>(cnt);
+        // the softmax sum with fm_route_kernel's arithmetic (the same per-wave
+        // sums added in wave order; waves past E add zeros), so p is bit-equal
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) sum += R.red[w];
+        inv = 1.0f / sum;
         if (act && r == 0) {
             const int pbits = __float_as_int(__int_as_float((int)(key >> 32)) * inv);
             if (cnt < K) {
@@ -877,7 +873,13 @@ FM_DEV float fmc_route(const FmDecodeArgs &a, FmcLds &L, const float *lgq, uint3
             if (cnt == K - 1) R.ek1 = (int)(key >> 32);
             if (cnt == K) R.vk = (int)(key >> 32);
         }
-    } else if (tid < NC) {
+    } else {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) sum += R.red[w];
+        inv = 1.0f / sum;
+    }
+    if (NC > FMC_THREADS / 8 && tid < NC) {
         const int v = R.cv[tid], me = R.ci[tid];
         int pos = 0;
         for (int j = 0; j < NC; j += 4) {
@@ -981,6 +983,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // counters first (no load is in flight yet, so this barrier is cheap)
     if (tid < FMC_NG) L.it[tid].sync = 0;
     if (tid < 4) L.hlp_done[tid] = 0;
+    if (RT && tid < FMC_THREADS / 8) L.rt.ck[tid] = 0;
     if (tid == 0) {
         L.xready = L.dn_ready = L.hlp_go = 0;
         if constexpr (RT) {
