@@ -1159,7 +1159,12 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     if (doA) {
         fmm_f4 g0 = {0, 0, 0, 0}, g1 = g0, u0 = g0, u1 = g0;
         const fm_h2 *xq = &L.xq[s.bits == 4 ? 0 : 1][NG * wv][0];
-        if (s.bits == 4) {
+        if (s.bits == 4 && grp == FMC_NG - 1) {
+            // the last item's gate/up MMA (its data arrives last) with the x
+            // operand from LDS: shorter per step when it runs alone on a SIMD
+            fmm_mma_l4<NG>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
+            fmm_mma_l4<NG>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
+        } else if (s.bits == 4) {
             fmm_mma<4, NG>(cg, xq, L.zero, T.tr[wv], g0, g1, lane);
             fmm_mma<4, NG>(cu, xq, L.zero, T.tr[wv], u0, u1, lane);
         } else {
