@@ -203,6 +203,30 @@ def test_encode_experts_batched_and_combine(orc, dev):
     assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32
 
 
+@pytest.mark.parametrize("bitmode", ["4", "mixed"])
+def test_encode_experts_batched_eleven(orc, dev, bitmode):
+    """Per-expert outputs (mode 1) with 11 experts: 704 tiles on 256 CUs, so
+    192 CUs hold a third item, whose 4-bit down rows are split with item 0's
+    waves; "mixed" gives third items of both widths."""
+    import torch
+    say("encode_experts_batched, 11 experts", bitmode)
+    n = 11
+    bl = [4] * n if bitmode == "4" else [4 if i % 2 == 0 else 2 for i in range(n)]
+    blobs, x, _, _, _ = _decode_inputs(17, n - 1, bl)
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
+    ws = fm.workspace(fm.decode_workspace_bytes(n, HIDDEN, INTER), dev)
+    eo = torch.full((n, HIDDEN), float("nan"), dtype=torch.float32, device=dev)
+    for rep in range(2):  # the second call reuses the workspace (next epoch)
+        fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
+        torch.cuda.synchronize()
+        eon = eo.cpu().numpy()
+        for k in range(n):
+            r = orc.expert_forward(blobs[k], bl[k], HIDDEN, INTER, x)
+            assert norm_err(eon[k], r) <= TOL_F32, (rep, k)
+    assert fm.workspace_status(ws) == 0
+
+
 @pytest.fixture(scope="module")
 def pool64(dev):
     """64 experts, tiered 4/2-bit (every fourth expert 4-bit), plus a shared expert."""
