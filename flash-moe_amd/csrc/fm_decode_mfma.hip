@@ -724,13 +724,6 @@ struct __attribute__((aligned(16))) FmcItem {
     uint32_t sync;                // the item's 4-wave barrier counter
 };
 
-#ifndef FMC_PT
-#define FMC_PT 512  // pool entries copied into LDS by the one-workgroup-per-CU kernel
-#endif
-#ifndef FMC_POOL_LDS
-#define FMC_POOL_LDS 0  // the pool tables copied into LDS at the start (see fm_decode_cu_kernel)
-#endif
-
 #ifndef FMC_DN_HELP
 #define FMC_DN_HELP 1  // item 0's waves take half of the last item's down MMA (see fm_decode_cu_kernel)
 #endif
@@ -775,8 +768,6 @@ struct __attribute__((aligned(16))) FmcLds {
     uint16_t dsb[4][2][16 * FMM_GI];       // ... and their scales / biases
     int rsel[FM_MAX_K];           // fused routing: expert of routed slot k (descending probability)
     int rp[FM_MAX_K];             // ... and its probability bits
-    uint64_t pt[FMC_PT];          // pool mode: the pool's blob addresses (experts < FMC_PT) ...
-    uint8_t pb8[FMC_PT];          // ... and bit widths
 };
 
 
@@ -1003,21 +994,6 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     __syncthreads();
     const uint32_t ep_ld = fm_epoch_load(a);
     constexpr bool fused = RT;
-    // Pool mode: the pool tables (and, without fused routing, idx / wdev)
-    // are loaded now, next to the logits and x, and read from LDS once the
-    // slots are known -- the slot lookup then waits for no memory round trip.
-    const bool ptab = FMC_POOL_LDS && a.pool_mode && a.pool_n <= FMC_PT;
-    const bool pidx = FMC_POOL_LDS && !RT && a.pool_mode;
-    uint64_t ptv = 0;
-    uint32_t pbv = 0, piv = 0, pwv = 0;
-    if (ptab && tid < (int)a.pool_n) {
-        ptv = (uint64_t)(uintptr_t)a.pool_blobs[tid];
-        pbv = a.pool_bits[tid];
-    }
-    if (pidx && tid < a.K) {
-        piv = (uint32_t)a.idx[tid];
-        pwv = __float_as_uint(a.wdev[tid]);
-    }
     float lgq[FMC_THREADS / 64];
     uint32_t etab = 0;  // exp table in lanes (fm_expf_lanes), loaded with the logits
     if constexpr (RT) {
@@ -1032,16 +1008,6 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     fm_f4 xr[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (gt < (int)GH * 4 ? gt : 0) + 4 * j);
-    if (ptab && tid < (int)a.pool_n) {
-        L.pt[tid] = ptv;
-        L.pb8[tid] = (uint8_t)pbv;
-    }
-    if (pidx && tid < a.K) {
-        L.rsel[tid] = (int)piv;
-        L.rp[tid] = (int)pwv;
-    }
-    // (fused routing: the routing's own barriers publish these stores)
-    if (pidx) __syncthreads();
     float winv = 1.f;
     if constexpr (RT) winv = fmc_route(a, L, lgq, etab);
     if (fused && blockIdx.x == gridDim.x - 1 && grp == FMC_NG - 1 && wv == 0) {
@@ -1069,11 +1035,8 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
             a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
         }
     }
-    // (without fused routing, L.rsel / L.rp hold idx / wdev: the weight is w * 1)
-    const int *rsel = (RT || pidx) ? L.rsel : nullptr;
-    const uint64_t *pt = ptab ? L.pt : nullptr;
-    const uint32_t ptn = ptab ? a.pool_n : 0;
-    const FmSlot s = fmc_slot(a, k, rsel, L.rp, winv, pt, L.pb8, ptn);
+    const int *rsel = RT ? L.rsel : nullptr;
+    const FmSlot s = fmc_slot(a, k, rsel, L.rp, winv);
     const bool doA = has && s.valid;
     // The last item's down rows: item 0's waves copy them into LDS right
     // after publishing their own activations, so they queue behind the gate/up
@@ -1090,7 +1053,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
     // right after its own down rows, and hands the partial sums over in LDS.
     // Only for 4-bit slots (one wave per SIMD becomes two).
     constexpr bool HLP = FMC_DN_HELP && NG == 16;
-    const FmSlot s_l = ((DNL || HLP) && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv, pt, L.pb8, ptn) : s;
+    const FmSlot s_l = ((DNL || HLP) && grp == 0) ? fmc_slot(a, k_l, rsel, L.rp, winv) : s;
     const bool help0 = HLP && grp == 0 && has_l && s_l.valid && s_l.bits == 4;
     const bool help2 = HLP && grp == FMC_NG - 1 && doA && s.bits == 4;
     const bool dn_lds = DNL && (grp == 0 ? has_l && s_l.valid : (grp == FMC_NG - 1 && doA));
@@ -1123,7 +1086,7 @@ __global__ __launch_bounds__(FMC_THREADS, 1) void fm_decode_cu_kernel(FmDecodeAr
 #pragma unroll
         for (int kk = 0; kk < FM_MAX_SLOTS; kk++) {
             if (kk < a.S) {
-                const FmSlot sk = fmc_slot(a, kk, rsel, L.rp, winv, pt, L.pb8, ptn);
+                const FmSlot sk = fmc_slot(a, kk, rsel, L.rp, winv);
                 if (lane == 0) L.it[grp].cw[kk] = sk.weight;
                 vm |= sk.valid ? 1u << kk : 0u;
             }

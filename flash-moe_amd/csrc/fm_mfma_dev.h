@@ -114,12 +114,9 @@ FM_DEV uint64_t fmc_ld64(const void *p) { return *(fmc_cu64 *)p; }
 
 // Slot k (wave-uniform) resolved with scalar loads: idx / weight, then the
 // pool's blob address and bit width.  With rsel (fused routing) the expert
-// and its probability come from LDS and the weight is p * winv.  With pt
-// (experts e < ptn) the blob address and bit width come from a copy of the
-// pool tables in LDS (pt / pb8) instead of a dependent scalar round trip.
+// and its probability come from LDS and the weight is p * winv.
 FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k, const int *rsel = nullptr, const int *rp = nullptr,
-                       float winv = 1.f, const uint64_t *pt = nullptr, const uint8_t *pb8 = nullptr,
-                       uint32_t ptn = 0) {
+                       float winv = 1.f) {
     if (!a.pool_mode || k >= a.K) return a.slot[k];
     FmSlot s;
     int e;
@@ -137,20 +134,9 @@ FM_DEV FmSlot fmc_slot(const FmDecodeArgs &a, int k, const int *rsel = nullptr, 
         s.weight = 0.f;
         return s;
     }
-    const char *blob;
-    int bits;
-    if (pt && (uint32_t)e < ptn) {
-        const uint64_t b = pt[e];
-        // (readfirstlane returns int: widen through uint32_t, no sign extension)
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-        blob = (const char *)(((uint64_t)hi << 32) | (uint64_t)lo);
-        bits = __builtin_amdgcn_readfirstlane(pb8[e]);
-    } else {
-        blob = (const char *)fmc_ld64(a.pool_blobs + e);
-        const uintptr_t bp = (uintptr_t)(a.pool_bits + e);
-        bits = (int)((fmc_ld32((const void *)(bp & ~(uintptr_t)3)) >> (8 * (bp & 3))) & 0xffu);
-    }
+    const char *blob = (const char *)fmc_ld64(a.pool_blobs + e);
+    const uintptr_t bp = (uintptr_t)(a.pool_bits + e);
+    const int bits = (int)((fmc_ld32((const void *)(bp & ~(uintptr_t)3)) >> (8 * (bp & 3))) & 0xffu);
     const uint64_t *off = bits == 2 ? a.off2 : a.off4;
     s.gw = (const uint32_t *)(blob + off[0]);
     s.gs = (const uint16_t *)(blob + off[1]);
