@@ -51,6 +51,8 @@ struct FmDecodeArgs {
     float *normed;           // fp32 [hidden]
     uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
     uint64_t *p2;            // few-slot kernel: [S][64 tiles][4 quarters][16 rows][gate, up] tagged partials
+    float *actf;             // row-split kernel: [S][inter] activations (untagged; guarded by flags)
+    uint64_t *flags;         // row-split kernel: [hidden / 16] tagged per-workgroup "activations stored" words
     // routing fused into the step (one token, pool mode, one-workgroup-per-CU
     // kernel): softmax / top-K / renormalise of route_logits in every
     // workgroup; idx / wdev are then unused, and the slot-order indices and
@@ -157,6 +159,7 @@ __device__ __forceinline__ void fm_epoch_publish(const FmDecodeArgs &a, uint32_t
 // each returns FM_ERR_UNSUPPORTED (message cleared by the caller) when the
 // shape or slot mix is outside what it implements.
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st);
+int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st);
 
 // Standalone RMS norm launch (fm_rms_norm's kernel) for paths without the fused one.
 int fm_launch_rms_norm(const float *x, const uint16_t *w, uint32_t dim, float eps, float *out, uint16_t *out_bf16,

@@ -1,0 +1,142 @@
+"""GPU parity of the row-split decode kernel (fm_decode_bal.hip: every CU owns
+4 intermediate rows and 16 output rows of every slot; one activation hand-off
+per CU, combine local to the CU).
+
+It is the kernel of a one-token step at hidden 4096 / inter 1024 with 2 to 11
+slots; FMOE_DECODE_NO_BAL=1 selects the per-CU item kernel instead.  Bars:
+fp32 output norm_err <= 1e-3 from the oracle; the two kernels within 1e-5 of
+each other (they differ only in the rounding of the activation group sums);
+bf16 output <= 2e-2.  Covers 4-bit, 2-bit and mixed-width gate/up tiles,
+steps with and without a shared expert, invalid routed slots, and the two
+kernels alternating on one workspace (one epoch shared by both).
+"""
+import numpy as np
+import pytest
+
+import fmoe_amd as fm
+from fmoe_amd import synth
+from helpers import HIDDEN, INTER, TOL_BF16, TOL_F32, bf16_out, experts, norm_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _bal_on(monkeypatch):
+    monkeypatch.setenv("FMOE_DECODE_BAL", "1")
+
+
+def T(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _bits(mode, n):
+    if mode in ("4", "2"):
+        return [int(mode)] * n
+    return [4 if i % 3 else 2 for i in range(n)]  # mixed: tiles of two widths
+
+
+def _step(orc, dev, K, mode, shared, seed, monkeypatch, valid=None):
+    import torch
+    n = K + (1 if shared else 0)
+    bl = _bits(mode, n)
+    blobs = experts(range(9100 + 20 * seed, 9100 + 20 * seed + n), bl)
+    rng = synth.rng_for(91, K, seed, sum(map(ord, mode)))
+    x = synth.hidden_vec(rng, HIDDEN)
+    hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+    w = rng.random(K).astype(np.float32)
+    w /= w.sum()
+    score = float(rng.normal())
+    dbl = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(d, bl[i], HIDDEN, INTER) for i, d in enumerate(dbl)]
+    ws = fm.workspace(fm.decode_workspace_bytes(n, HIDDEN, INTER), dev)
+    outs = {}
+    for kern in ("bal", "cu"):
+        if kern == "cu":
+            monkeypatch.setenv("FMOE_DECODE_NO_BAL", "1")
+        else:
+            monkeypatch.delenv("FMOE_DECODE_NO_BAL", raising=False)
+        out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+        ob = torch.empty(HIDDEN, dtype=torch.int16, device=dev)
+        fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, valid=valid,
+                      shared=ex[K] if shared else None, shared_bits=bl[K] if shared else 4, shared_score=score,
+                      h_mid=T(hm, dev), out_bf16=ob)
+        torch.cuda.synchronize()
+        outs[kern] = (out.cpu().numpy(), bf16_out(ob.cpu().numpy()))
+    monkeypatch.delenv("FMOE_DECODE_NO_BAL", raising=False)
+    assert fm.workspace_status(ws) == 0
+    keep = [k for k in range(K) if valid is None or valid[k]]
+    ref = orc.moe_decode([blobs[k] for k in keep], [bl[k] for k in keep], w[keep], x, HIDDEN, INTER,
+                         shared_blob=blobs[K] if shared else None, shared_bits=bl[K] if shared else 4,
+                         shared_score=score if shared else 0.0, h_mid=hm)
+    got, gotb = outs["bal"]
+    assert norm_err(got - hm, ref - hm) <= TOL_F32
+    assert norm_err(gotb, ref) <= TOL_BF16
+    assert norm_err(got - hm, outs["cu"][0] - hm) <= 1e-5
+
+
+@pytest.mark.parametrize("mode", ["4", "2", "mixed"])
+@pytest.mark.parametrize("K,shared", [(10, True), (10, False), (7, True), (4, True), (1, True), (11, False)])
+def test_bal_step(orc, dev, monkeypatch, K, shared, mode):
+    say("bal decode", K, shared, mode)
+    _step(orc, dev, K, mode, shared, 0, monkeypatch)
+
+
+def test_bal_invalid_slots(orc, dev, monkeypatch):
+    say("bal decode: invalid routed slots")
+    _step(orc, dev, 10, "mixed", True, 1, monkeypatch, valid=[1, 0, 1, 1, 0, 1, 1, 1, 1, 0])
+
+
+def test_bal_and_cu_alternate_on_one_workspace(orc, dev, monkeypatch):
+    """Pool steps that alternate the row-split kernel, the per-CU item kernel
+    and the fused-routing row-split kernel on one workspace: each is checked
+    against the oracle, so a stale hand-off word from another kernel's call
+    would show."""
+    import torch
+    say("bal / cu alternating on one workspace")
+    E, K = 64, 10
+    bits = [4, 2, 4, 4, 2, 4, 4, 2]
+    blobs = experts(range(9300, 9300 + len(bits)), bits)
+    n = len(blobs)
+    dp = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    dp.blob_table = torch.from_numpy(np.array([dp.addrs[e % n] for e in range(E)], np.int64)).to(dev)
+    dp.bits_table = torch.from_numpy(np.array([bits[e % n] for e in range(E)], np.uint8)).to(dev)
+    dp.c = fm.ExpertPool(dp.blob_table.data_ptr(), dp.bits_table.data_ptr(), E, HIDDEN, INTER, 64)
+    sh_blob = synth.expert_blob((9400, 1), HIDDEN, INTER, 4)
+    dsh = T(sh_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+    w = torch.empty((1, K), dtype=torch.float32, device=dev)
+    ridx = torch.empty(K, dtype=torch.int32, device=dev)
+    rw = torch.empty(K, dtype=torch.float32, device=dev)
+    rng = synth.rng_for(93)
+    for step, kern in enumerate(["bal", "cu", "bal", "fused", "cu", "fused", "bal", "bal"]):
+        lg = rng.normal(0, 1, E).astype(np.float32)
+        x = synth.hidden_vec(rng, HIDDEN)
+        g = np.array([rng.normal()], np.float32)
+        if kern == "cu":
+            monkeypatch.setenv("FMOE_DECODE_NO_BAL", "1")
+        else:
+            monkeypatch.delenv("FMOE_DECODE_NO_BAL", raising=False)
+        kw = dict(shared=sh, shared_bits=4, shared_score=T(g, dev))
+        if kern == "fused":
+            fm.moe_route_decode_pool(dp, T(lg, dev), ridx, rw, T(x, dev), out, ws, **kw)
+        else:
+            fm.route_topk(T(lg, dev).view(1, E), K, idx, w)
+            fm.moe_decode_pool(dp, idx[0], w[0], T(x, dev), out, ws, **kw)
+        torch.cuda.synchronize()
+        ri, rwt = orc.route(lg[None, :], K)
+        ref = orc.moe_decode([blobs[e % n] for e in ri[0]], [bits[e % n] for e in ri[0]], rwt[0], x, HIDDEN, INTER,
+                             shared_blob=sh_blob, shared_bits=4, shared_score=float(g[0]))
+        assert norm_err(out.cpu().numpy(), ref) <= TOL_F32, (step, kern)
+        if kern == "fused":
+            assert np.array_equal(ridx.cpu().numpy(), ri[0]), step
+            assert np.array_equal(rw.cpu().numpy().view(np.uint32), rwt[0].view(np.uint32)), step
+    monkeypatch.delenv("FMOE_DECODE_NO_BAL", raising=False)
+    assert fm.workspace_status(ws) == 0
