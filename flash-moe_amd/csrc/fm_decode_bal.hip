@@ -492,7 +492,7 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     }
 }
 
-// hidden 4096 / inter 1024, one token of 2 .. 11 slots (K routed + shared),
+// hidden 4096 / inter 1024, one token of 1 .. 11 slots (K routed + shared),
 // no fused norm: one workgroup per CU for the 256 row blocks (every one must
 // be resident: each waits for all the others' activations).
 int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
@@ -500,7 +500,7 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
     // FMOE_DECODE_NO_BAL set: off
     const char *on = getenv("FMOE_DECODE_BAL"), *off = getenv("FMOE_DECODE_NO_BAL");
     if (!(on && *on == '1') || (off && *off)) return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: disabled");
-    if (a.hidden != FMM_H || a.inter != FMM_MAXI || a.ntok > 1 || a.S < 2 || a.S > FMB_MAXS || a.norm_w ||
+    if (a.hidden != FMM_H || a.inter != FMM_MAXI || a.ntok > 1 || a.S < 1 || a.S > FMB_MAXS || a.norm_w ||
         !a.actf || !a.flags)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: shape");
     if (a.route_logits && !(a.mode == 0 && a.pool_mode && a.K >= 1 && a.K <= 64 && a.route_E >= a.K &&

@@ -1889,6 +1889,12 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
+    // one token of up to 11 slots: the row-split kernel where it is enabled
+    if (a.ntok <= 1) {
+        const int rc = fm_launch_decode_bal(a, st);
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
+    }
     // up to four slots of one token (no fused norm): the split kernel
     if (a.ntok <= 1 && a.S <= FMS_MAXS && !a.norm_w && !a.route_logits) {
         const char *no_split = getenv("FMOE_DECODE_NO_SPLIT");
@@ -1902,13 +1908,6 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
             hipLaunchKernelGGL(fm_decode_split_kernel, dim3(FMS_GRID), dim3(256), 0, st, a);
             return fm_check_launch("fm_decode_split_kernel");
         }
-    }
-    // one token of up to 11 slots: the row-split kernel (FMOE_DECODE_NO_BAL set:
-    // the per-CU item kernel below, which tests compare it with)
-    if (a.ntok <= 1) {
-        const int rc = fm_launch_decode_bal(a, st);
-        if (rc != FM_ERR_UNSUPPORTED) return rc;
-        fm_clear_error();
     }
     static int per_cu_c = -1;
     if (per_cu_c < 0 &&
