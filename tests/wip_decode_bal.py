@@ -140,3 +140,35 @@ def test_bal_and_cu_alternate_on_one_workspace(orc, dev, monkeypatch):
             assert np.array_equal(rw.cpu().numpy().view(np.uint32), rwt[0].view(np.uint32)), step
     monkeypatch.delenv("FMOE_DECODE_NO_BAL", raising=False)
     assert fm.workspace_status(ws) == 0
+
+
+@pytest.mark.parametrize("regime", ["1e-3", "1e2", "outliers", "mixed"])
+def test_bal_range(orc, dev, regime):
+    """Inputs outside N(0,1) (the regimes of test_gpu_range.py) through the
+    row-split kernel: the combined step and the per-expert outputs (mode 1),
+    mixed bit widths, 10 routed slots + shared."""
+    import torch
+    from test_gpu_range import REGIMES, x_regime
+    say("bal range", regime)
+    K = 10
+    bl = [4, 2, 4, 4, 2, 4, 2, 4, 4, 2, 4]
+    blobs = experts(range(9500, 9500 + K + 1), bl)
+    rng = synth.rng_for(95, REGIMES.index(regime))
+    x = x_regime(rng, HIDDEN, regime)
+    w = orc.route(rng.normal(0, 1, 64).astype(np.float32), K)[1][0]
+    dblobs = [T(b, dev) for b in blobs]
+    ex = [fm.experts_from_blob(db, bl[i], HIDDEN, INTER) for i, db in enumerate(dblobs)]
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    eo = torch.zeros((K + 1, HIDDEN), dtype=torch.float32, device=dev)
+    fm.encode_experts_batched(ex, bl, T(x, dev), eo, ws, HIDDEN, INTER)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    fm.moe_decode(ex[:K], bl[:K], w, T(x, dev), out, ws, HIDDEN, INTER, shared=ex[K], shared_bits=bl[K],
+                  shared_score=0.7)
+    torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
+    eon = eo.cpu().numpy()
+    for k in range(K + 1):
+        assert norm_err(eon[k], orc.expert_forward(blobs[k], bl[k], HIDDEN, INTER, x)) <= TOL_F32, k
+    ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, shared_blob=blobs[K], shared_bits=bl[K],
+                         shared_score=0.7)
+    assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
