@@ -52,7 +52,7 @@ struct FmDecodeArgs {
     uint64_t *ss2;           // [hidden/64] tagged partial sums of squares
     uint64_t *p2;            // few-slot kernel: [S][64 tiles][4 quarters][16 rows][gate, up] tagged partials
     float *actf;             // row-split kernel: [S][inter] activations (untagged; guarded by flags)
-    uint64_t *flags;         // row-split kernel: [hidden / 16] tagged per-workgroup "activations stored" words
+    uint64_t *flags;         // row-split kernel: [hidden / 16] tagged "activations stored" words, then [hidden / 16] norm partials
     // routing fused into the step (one token, pool mode, one-workgroup-per-CU
     // kernel): softmax / top-K / renormalise of route_logits in every
     // workgroup; idx / wdev are then unused, and the slot-order indices and

@@ -715,13 +715,14 @@ static int fm_check_expert(const char *who, int k, const fm_expert_weights &e, i
 // [ss2: hidden/64 x 8 B tagged partial sums of squares for the fused RMS norm]
 // It starts zeroed (fm_workspace_init); tags make stale contents harmless after that.
 // [p2: up to 4 slots x inter/16 tiles x 4 quarters x 32 tagged partial sums (the few-slot kernel)]
-// [actf: S x inter x 4 B activations] [flags: hidden/16 x 8 B tagged] (the row-split kernel)
+// [actf: S x inter x 4 B activations] [flags: 2 x hidden/16 x 8 B tagged: activation
+//  flags, then norm partial sums] (the row-split kernel)
 extern "C" size_t fm_moe_decode_workspace_size(int n_slots, uint32_t hidden, uint32_t inter) {
     if (n_slots < 1) n_slots = 1;
     const size_t few = n_slots < 4 ? n_slots : 4;
     return 256 + fm_align_up((size_t)n_slots * inter * 8, 256) + fm_align_up((size_t)n_slots * hidden * 8, 256) +
            fm_align_up((size_t)(hidden + 63) / 64 * 8, 256) + fm_align_up(few * (inter / 16) * 4 * 32 * 8, 256) +
-           fm_align_up((size_t)n_slots * inter * 4, 256) + fm_align_up((size_t)(hidden + 15) / 16 * 8, 256);
+           fm_align_up((size_t)n_slots * inter * 4, 256) + fm_align_up((size_t)(hidden + 15) / 16 * 16, 256);
 }
 
 template <int LH, int GH, int LI, int GI>

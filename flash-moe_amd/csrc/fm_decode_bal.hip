@@ -470,20 +470,51 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     // ---- wave 0: the combine of the CU's 16 rows over every slot, in slot order ----
     if (wv == 0 && a.mode == 0) {
         fmb_wait_lds(a, &L.ydone, (uint32_t)S);
+        const uint32_t row = 16 * c + n;
+        float o = 0.f;
         if (lane < 16) {
-            const uint32_t row = 16 * c + lane;
             const uint32_t cv = L.cvalid;
             float moe = 0.f;
 #pragma unroll
             for (int kk = 0; kk < FM_MAX_SLOTS; kk++)
                 if (kk < a.K && ((cv >> kk) & 1u)) moe = __fadd_rn(moe, __fmul_rn(L.cw[kk], L.y[kk][lane]));
-            float o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
+            o = a.h_mid ? __fadd_rn(a.h_mid[row], moe) : moe;
             if (a.has_shared)
                 o = __fadd_rn(o, __fmul_rn(L.sw, L.y[S - 1][lane]));
             else if (a.shared_y)
                 o = __fadd_rn(o, __fmul_rn(L.sw, a.shared_y[row]));
             a.out[row] = o;
             if (a.out_bf16) a.out_bf16[row] = fm_f32_to_bf16(o);
+        }
+        if (a.norm_w) {
+            // next layer's input RMS norm (cpu_kernels.h:235-246): every CU
+            // publishes the sum of squares of its 16 rows (tagged), then every
+            // CU adds all of them in the same fixed order (all 64 lanes here)
+            const float sq = fm_lane_sum<16>(lane < 16 ? o * o : 0.f);
+            const uint32_t G = gridDim.x;
+            uint64_t *ssq = a.flags + G;
+            if (lane == 0) fm_put_tagged(&ssq[c], sq, ep);
+            uint64_t t[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                t[j] = 64 * j + lane < (int)G ? fm_get_tagged(&ssq[64 * j + lane]) : ((uint64_t)ep << 32);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int j = 0; j < 4; j++) ready &= (uint32_t)(t[j] >> 32) == ep;
+                if (__all(ready)) break;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if ((uint32_t)(t[j] >> 32) != ep) t[j] = fm_get_tagged(&ssq[64 * j + lane]);
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) part += 64 * j + lane < (int)G ? __uint_as_float((uint32_t)t[j]) : 0.f;
+            const float tot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(part))));
+            const float inv = 1.0f / sqrtf(tot / (float)FMM_H + a.norm_eps);
+            if (lane < 16) a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
         }
     }
     if (a.pool_mode && !RT && c == 0 && tid < a.K) {
@@ -500,7 +531,7 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
     // FMOE_DECODE_NO_BAL set: off
     const char *on = getenv("FMOE_DECODE_BAL"), *off = getenv("FMOE_DECODE_NO_BAL");
     if (!(on && *on == '1') || (off && *off)) return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: disabled");
-    if (a.hidden != FMM_H || a.inter != FMM_MAXI || a.ntok > 1 || a.S < 1 || a.S > FMB_MAXS || a.norm_w ||
+    if (a.hidden != FMM_H || a.inter != FMM_MAXI || a.ntok > 1 || a.S < 1 || a.S > FMB_MAXS || (a.norm_w && a.mode != 0) ||
         !a.actf || !a.flags)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: shape");
     if (a.route_logits && !(a.mode == 0 && a.pool_mode && a.K >= 1 && a.K <= 64 && a.route_E >= a.K &&

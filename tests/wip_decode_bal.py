@@ -172,3 +172,44 @@ def test_bal_range(orc, dev, regime):
     ref = orc.moe_decode(blobs[:K], bl[:K], w, x, HIDDEN, INTER, shared_blob=blobs[K], shared_bits=bl[K],
                          shared_score=0.7)
     assert norm_err(out.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_bal_norm(orc, dev):
+    """The step with the next layer's RMS norm fused (a second round of tagged
+    per-CU partial sums), pool-routed, tiered pool, 2-bit shared expert, three
+    calls on one workspace."""
+    import torch
+    say("bal decode + fused norm")
+    E, K = 64, 10
+    bits = [4, 2, 4, 4, 2, 4, 4, 2]
+    blobs = experts(range(9600, 9600 + len(bits)), bits)
+    n = len(blobs)
+    dp = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    dp.blob_table = torch.from_numpy(np.array([dp.addrs[e % n] for e in range(E)], np.int64)).to(dev)
+    dp.bits_table = torch.from_numpy(np.array([bits[e % n] for e in range(E)], np.uint8)).to(dev)
+    dp.c = fm.ExpertPool(dp.blob_table.data_ptr(), dp.bits_table.data_ptr(), E, HIDDEN, INTER, 64)
+    rng = synth.rng_for(96)
+    shared_blob = synth.expert_blob((9700, 1), HIDDEN, INTER, 2)
+    dsh = T(shared_blob, dev)
+    sh = fm.experts_from_blob(dsh, 2, HIDDEN, INTER)
+    ws = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    normed = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+    idx = torch.empty((1, K), dtype=torch.int32, device=dev)
+    w = torch.empty((1, K), dtype=torch.float32, device=dev)
+    for rep in range(3):
+        lg = rng.normal(0, 1, (1, E)).astype(np.float32)
+        x = synth.hidden_vec(rng, HIDDEN)
+        hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
+        nw = synth.bf16_bits(rng.normal(1, 0.2, HIDDEN).astype(np.float32))
+        g = T(np.array([-0.4], np.float32), dev)
+        fm.route_topk(T(lg, dev), K, idx, w)
+        fm.moe_decode_pool_norm(dp, idx, w, T(x, dev), out, ws, T(nw.view(np.int16), dev), 1e-6, normed, shared=sh,
+                                shared_bits=2, shared_score=g, h_mid=T(hm, dev))
+        torch.cuda.synchronize()
+        ri, rw = orc.route(lg, K)
+        ref = orc.moe_decode([blobs[e % n] for e in ri[0]], [bits[e % n] for e in ri[0]], rw[0], x, HIDDEN, INTER,
+                             shared_blob=shared_blob, shared_bits=2, shared_score=-0.4, h_mid=hm)
+        assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, rep
+        assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, nw, 1e-6)) <= TOL_F32, rep
+    assert fm.workspace_status(ws) == 0
