@@ -523,17 +523,22 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     }
 }
 
-// hidden 4096 / inter 1024, one token of 1 .. 11 slots (K routed + shared),
-// no fused norm: one workgroup per CU for the 256 row blocks (every one must
-// be resident: each waits for all the others' activations).
+// hidden 4096 / inter 1024, 1 .. 11 slots a token, no fused norm with several
+// tokens: one workgroup per CU for the 256 row blocks (every one must be
+// resident: each waits for all the others' activations).  Several tokens (pool
+// mode, the combine) run as one launch per token on the same workspace (each
+// launch tags with its own epoch).
 int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
     // opt-in (FMOE_DECODE_BAL=1) until it has been measured on the GPU;
     // FMOE_DECODE_NO_BAL set: off
     const char *on = getenv("FMOE_DECODE_BAL"), *off = getenv("FMOE_DECODE_NO_BAL");
     if (!(on && *on == '1') || (off && *off)) return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: disabled");
-    if (a.hidden != FMM_H || a.inter != FMM_MAXI || a.ntok > 1 || a.S < 1 || a.S > FMB_MAXS || (a.norm_w && a.mode != 0) ||
+    const int ntok = a.ntok > 1 ? a.ntok : 1, spt = ntok > 1 ? a.spt : a.S;
+    if (a.hidden != FMM_H || a.inter != FMM_MAXI || spt < 1 || spt > FMB_MAXS || (a.norm_w && a.mode != 0) ||
         !a.actf || !a.flags)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: shape");
+    if (ntok > 1 && (!a.pool_mode || a.mode != 0 || a.norm_w || a.route_logits || a.S != ntok * spt))
+        return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: several tokens need pool mode and the combine");
     if (a.route_logits && !(a.mode == 0 && a.pool_mode && a.K >= 1 && a.K <= 64 && a.route_E >= a.K &&
                             a.route_E <= FMC_THREADS))
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: fused routing");
@@ -544,9 +549,25 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
         per_cu = 0;
     if (per_cu < 1 || (uint32_t)(per_cu * fm_num_cus()) < grid)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: %u workgroups not resident", grid);
-    if (a.route_logits)
-        hipLaunchKernelGGL(fm_decode_bal_kernel<true>, dim3(grid), dim3(FMB_THREADS), 0, st, a);
-    else
-        hipLaunchKernelGGL(fm_decode_bal_kernel<false>, dim3(grid), dim3(FMB_THREADS), 0, st, a);
-    return fm_check_launch("fm_decode_bal_kernel");
+    for (int t = 0; t < ntok; t++) {
+        FmDecodeArgs b = a;
+        if (ntok > 1) {
+            b.ntok = 1;
+            b.spt = b.S = spt;
+            b.idx = a.idx + (size_t)t * a.K;
+            b.wdev = a.wdev + (size_t)t * a.K;
+            b.x = a.x + (size_t)t * FMM_H;
+            b.out = a.out + (size_t)t * FMM_H;
+            if (a.h_mid) b.h_mid = a.h_mid + (size_t)t * FMM_H;
+            if (a.out_bf16) b.out_bf16 = a.out_bf16 + (size_t)t * FMM_H;
+            if (a.shared_score) b.shared_score = a.shared_score + t;
+        }
+        if (b.route_logits)
+            hipLaunchKernelGGL(fm_decode_bal_kernel<true>, dim3(grid), dim3(FMB_THREADS), 0, st, b);
+        else
+            hipLaunchKernelGGL(fm_decode_bal_kernel<false>, dim3(grid), dim3(FMB_THREADS), 0, st, b);
+        const int rc = fm_check_launch("fm_decode_bal_kernel");
+        if (rc) return rc;
+    }
+    return FM_OK;
 }

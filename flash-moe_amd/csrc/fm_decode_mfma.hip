@@ -1889,8 +1889,8 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
-    // one token of up to 11 slots: the row-split kernel where it is enabled
-    if (a.ntok <= 1) {
+    // up to 11 slots a token: the row-split kernel where it is enabled
+    {
         const int rc = fm_launch_decode_bal(a, st);
         if (rc != FM_ERR_UNSUPPORTED) return rc;
         fm_clear_error();

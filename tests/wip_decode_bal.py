@@ -213,3 +213,43 @@ def test_bal_norm(orc, dev):
         assert norm_err(out.cpu().numpy() - hm, ref - hm) <= TOL_F32, rep
         assert norm_err(normed.cpu().numpy(), orc.rms_norm(ref, nw, 1e-6)) <= TOL_F32, rep
     assert fm.workspace_status(ws) == 0
+
+
+@pytest.mark.parametrize("Tn,K", [(2, 10), (4, 10), (8, 10), (3, 16)])
+def test_bal_few_tokens(orc, dev, Tn, K):
+    """A few tokens (fm_prefill_moe with T <= 8 runs decode steps): with the
+    row-split kernel one launch per token (K = 16 + shared is beyond its 11
+    slots and takes the multi-pass kernel); bit-equal to one fm_moe_decode_pool
+    call per token and within the bars of the oracle."""
+    import torch
+    say("bal few tokens", Tn, K)
+    E = 64
+    bits = [4 if e % 3 else 2 for e in range(E)]
+    blobs = experts(range(9800, 9800 + E), bits)
+    pool = fm.DevicePool(blobs, bits, HIDDEN, INTER)
+    rng = synth.rng_for(98, Tn, K)
+    idx, w = orc.route(rng.normal(0, 1, (Tn, E)).astype(np.float32), K)
+    X = synth.hidden_vec(rng, HIDDEN, (Tn, HIDDEN))
+    hm = rng.normal(0, 1, (Tn, HIDDEN)).astype(np.float32)
+    g = rng.normal(0, 1, Tn).astype(np.float32)
+    sh_blob = synth.expert_blob((9801, 0), HIDDEN, INTER, 4)
+    dsh = T(sh_blob, dev)
+    sh = fm.experts_from_blob(dsh, 4, HIDDEN, INTER)
+    ws = fm.workspace(fm.prefill_workspace_bytes(Tn, K, pool), dev)
+    fm.workspace_status(ws)
+    out = torch.empty((Tn, HIDDEN), dtype=torch.float32, device=dev)
+    fm.prefill_moe(pool, T(idx, dev), T(w, dev), T(X, dev), out, ws, shared=sh, shared_bits=4,
+                   shared_scores=T(g, dev), h_mid=T(hm, dev))
+    torch.cuda.synchronize()
+    assert fm.workspace_status(ws) == 0
+    got = out.cpu().numpy()
+    ws1 = fm.workspace(fm.decode_workspace_bytes(K + 1, HIDDEN, INTER), dev)
+    for t in range(Tn):
+        o = torch.empty(HIDDEN, dtype=torch.float32, device=dev)
+        fm.moe_decode_pool(pool, T(idx[t], dev), T(w[t], dev), T(X[t], dev), o, ws1, shared=sh, shared_bits=4,
+                           shared_score=T(g[t:t + 1], dev), h_mid=T(hm[t], dev))
+        torch.cuda.synchronize()
+        assert np.array_equal(got[t], o.cpu().numpy()), t
+    ref = orc.prefill_moe(idx, w, blobs, bits, X, HIDDEN, INTER, shared_blob=sh_blob, shared_bits=4,
+                          shared_scores=g, h_mid=hm)
+    assert norm_err(got - hm, ref - hm) <= TOL_F32
