@@ -344,10 +344,8 @@ template <bool MP>
 __global__ __launch_bounds__(256, MP ? 2 : FMM_BLOCKS_PER_CU) void fm_decode_mfma_kernel(FmDecodeArgs a_) {
     const FmDecodeArgs &a = a_;
     __shared__ FmmLds<MP ? FMM_MAXS : FM_MAX_SLOTS> L;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int n = lane & 15, q = lane >> 4;
+    const int tid = threadIdx.x;
     const uint32_t H = a.hidden, I = a.inter;
-    const uint32_t GI = I / 64;
     const uint32_t tilesA = I / 16, tilesB = H / 64;
     const int spt = a.spt;
     // Work items: item i is A tile i and B tile i (slot i / tiles).  The grid
@@ -1298,7 +1296,7 @@ __global__ __launch_bounds__(256, 1) void fm_decode_split_kernel(FmDecodeArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave's slot
     const int n = lane & 15, q = lane >> 4;
-    constexpr uint32_t H = FMM_H, I = FMM_MAXI, GI = FMM_MAXI / 64;
+    constexpr uint32_t H = FMM_H, I = FMM_MAXI;
     const uint32_t g = blockIdx.x, tile = g >> 2, quarter = g & 3;
     const uint32_t rowA0 = tile * 16, rowB0 = g * 16;
     const bool mine = wv < a.S;
