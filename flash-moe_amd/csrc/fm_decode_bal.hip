@@ -222,7 +222,10 @@ FM_DEV void fmb_build_group(const float (&v)[16], int qq, int bits, fm_h2 *dst, 
     }
 }
 
-template <bool RT>  // RT: routing fused into the launch (FmDecodeArgs::route_logits)
+// RT: routing fused into the launch (FmDecodeArgs::route_logits).
+// TAG: the activations are handed off as tagged words that each down wave
+// polls (no flag round); otherwise as plain words behind one flag per CU.
+template <bool RT, bool TAG>
 __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeArgs a) {
     __shared__ FmbLds L;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -373,6 +376,23 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     if (has0) unit_mma(u0, bA0, bB0, t0);
     if (has1) unit_mma(u1, bA1, bB1, t1);
     fmb_arrive(&L.pdone);
+    if (RT && wv == FMB_GU - 1 && c == gridDim.x - 1) {
+        // cpu_topk's slot order by serial replay, then cpu_normalize_weights
+        // (sequential sum over the slots): bit-equal to fm_route_kernel.  This
+        // wave holds no down tile (S <= 11), so the replay is off every chain.
+        __builtin_amdgcn_s_setprio(3);
+        const float pinv = L.rt.pconv ? 0.f : 1.0f / fm_serial_sum((const float *)L.rt.pb, a.route_E);
+        fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt, pinv);
+        __builtin_amdgcn_s_setprio(0);
+        fm_wave_lds_sync();
+        if (lane < a.K) {
+            float sm = 0.f;
+            for (int kk = 0; kk < a.K; kk++) sm += L.rt.s_val[kk];
+            const float v = L.rt.s_val[lane];
+            a.route_idx[lane] = L.rt.s_id[lane];
+            a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
+        }
+    }
 
     // ---- wave 0: SwiGLU of the CU's 4 S activations, publish, then wait for every CU ----
     float *actf = a.actf;
@@ -386,29 +406,18 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
             const uint32_t i = 4 * c + rr;
             // stored at 64 (i % 16) + i / 16: a reader lane l then holds
             // elements 16 l .. 16 l + 15 with 16 fully coalesced loads
-            if (s < S)
-                __hip_atomic_store(&actf[(size_t)s * I + 64 * (i & 15) + (i >> 4)], fm_silu_mul(g, u),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the activations are at the coherence point
-        if (lane == 0) fm_put_tagged(&a.flags[c], 0.f, ep);
-        if (RT && c == gridDim.x - 1) {
-            // cpu_topk's slot order by serial replay, then cpu_normalize_weights
-            // (sequential sum over the slots): bit-equal to fm_route_kernel.
-            // Here it overlaps this wave's wait for the other CUs.
-            __builtin_amdgcn_s_setprio(3);
-            const float pinv = L.rt.pconv ? 0.f : 1.0f / fm_serial_sum((const float *)L.rt.pb, a.route_E);
-            fm_topk_serial(L.rt.pb, a.route_E, a.K, L.rt, pinv);
-            __builtin_amdgcn_s_setprio(0);
-            fm_wave_lds_sync();
-            if (lane < a.K) {
-                float sm = 0.f;
-                for (int kk = 0; kk < a.K; kk++) sm += L.rt.s_val[kk];
-                const float v = L.rt.s_val[lane];
-                a.route_idx[lane] = L.rt.s_id[lane];
-                a.route_w[lane] = sm > 0.f ? v * (1.0f / sm) : v;
+            const size_t pos = (size_t)s * I + 64 * (i & 15) + (i >> 4);
+            if (s < S) {
+                if (TAG)
+                    fm_put_tagged(&a.act2[pos], fm_silu_mul(g, u), ep);
+                else
+                    __hip_atomic_store(&actf[pos], fm_silu_mul(g, u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+    }
+    if (!TAG && wv == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the activations are at the coherence point
+        if (lane == 0) fm_put_tagged(&a.flags[c], 0.f, ep);
         const uint32_t G = gridDim.x;
         uint64_t t[4];
 #pragma unroll
@@ -433,11 +442,36 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
 
     // ---- down: the slot's activations -> operand rows, 16 down rows from LDS ----
     if (down) {
-        fmb_wait_lds(a, &L.go, 1);
         float v[16];
+        if constexpr (TAG) {
+            // the slot's 1024 tagged activations (every CU stored 4 of them)
+            const uint64_t *src = a.act2 + (size_t)sd * I + lane;
+            uint64_t t[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            v[i] = __hip_atomic_load(&actf[(size_t)sd * I + 64 * i + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 16; i++) t[i] = fm_get_tagged(src + 64 * i);
+            uint32_t it = 0;
+            do {
+                bool ready = true;
+#pragma unroll
+                for (int i = 0; i < 16; i++) ready &= (uint32_t)(t[i] >> 32) == ep;
+                if (__all(ready)) break;
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if ((uint32_t)(t[i] >> 32) != ep) t[i] = fm_get_tagged(src + 64 * i);
+            } while (++it < FM_SPIN_MAX);
+            if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = __uint_as_float((uint32_t)t[i]);
+            // slot sd's activations come from every CU, and every CU's wave 0
+            // read the epoch before storing them: publish it for the next call
+            if (sd == 0 && c == 0 && lane == 0) fm_epoch_publish(a, ep);
+        } else {
+            fmb_wait_lds(a, &L.go, 1);
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                v[i] = __hip_atomic_load(&actf[(size_t)sd * I + 64 * i + lane], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        }
         float y = 0.f;
         if (okD) {
             fmb_build_group(v, lane & 3, sD.bits, &L.aq[sd][lane >> 2][0], &L.asum[sd][lane >> 2],
@@ -545,10 +579,13 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
     const uint32_t grid = FMM_H / 16;
     static int per_cu = -1;
     if (per_cu < 0 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_bal_kernel<false>, FMB_THREADS, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_bal_kernel<false, false>, FMB_THREADS, 0) != hipSuccess)
         per_cu = 0;
     if (per_cu < 1 || (uint32_t)(per_cu * fm_num_cus()) < grid)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: %u workgroups not resident", grid);
+    // FMOE_BAL_TAGGED=1: the tagged-activation hand-off (measured against the flag round)
+    const char *tg = getenv("FMOE_BAL_TAGGED");
+    const bool tagged = tg && *tg == '1';
     for (int t = 0; t < ntok; t++) {
         FmDecodeArgs b = a;
         if (ntok > 1) {
@@ -562,10 +599,10 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
             if (a.out_bf16) b.out_bf16 = a.out_bf16 + (size_t)t * FMM_H;
             if (a.shared_score) b.shared_score = a.shared_score + t;
         }
-        if (b.route_logits)
-            hipLaunchKernelGGL(fm_decode_bal_kernel<true>, dim3(grid), dim3(FMB_THREADS), 0, st, b);
-        else
-            hipLaunchKernelGGL(fm_decode_bal_kernel<false>, dim3(grid), dim3(FMB_THREADS), 0, st, b);
+        void (*kern)(FmDecodeArgs) =
+            b.route_logits ? (tagged ? fm_decode_bal_kernel<true, true> : fm_decode_bal_kernel<true, false>)
+                           : (tagged ? fm_decode_bal_kernel<false, true> : fm_decode_bal_kernel<false, false>);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(FMB_THREADS), 0, st, b);
         const int rc = fm_check_launch("fm_decode_bal_kernel");
         if (rc) return rc;
     }

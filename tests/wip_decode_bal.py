@@ -20,9 +20,11 @@ from helpers import HIDDEN, INTER, TOL_BF16, TOL_F32, bf16_out, experts, norm_er
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True)
-def _bal_on(monkeypatch):
+@pytest.fixture(autouse=True, params=["flag", "tagged"])
+def _bal_on(monkeypatch, request):
+    """Both activation hand-offs: one flag word per CU, or tagged activations."""
     monkeypatch.setenv("FMOE_DECODE_BAL", "1")
+    monkeypatch.setenv("FMOE_BAL_TAGGED", "1" if request.param == "tagged" else "0")
 
 
 def T(a, dev):
