@@ -56,6 +56,14 @@ def pmc_traffic(name):
     return round(d["fetch_kib"] * 1024 * d["fetch_scale"] + d["write_kib"] * 1024 * d["write_scale"])
 
 
+def _decode_kernel_name(fused):
+    """The kernel a one-token config-2 step runs: the row-split kernel where the
+    library's switch enables it (FMOE_DECODE_BAL=1), else the per-CU item kernel."""
+    bal = os.environ.get("FMOE_DECODE_BAL") == "1" and not os.environ.get("FMOE_DECODE_NO_BAL")
+    tag = "true" if fused else "false"
+    return f"fm_decode_bal_kernel<{tag}, false>" if bal else f"fm_decode_cu_kernel<16, {tag}>"
+
+
 def graph_of(step, items):
     """step(i) for every i in items recorded into one HIP graph (on a side
     stream, as stream capture requires).  Replaying it runs exactly those
@@ -222,9 +230,9 @@ def bench_decode(args, dev):
         "value": step_bytes / (fused_ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": fused_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": fused_gbs / HBM_PEAK_GBS, "traffic": pmc_traffic("decode_fused_config2_pmc.json"),
-                     "kernel": "fm_decode_cu_kernel<16, true> (one fm_moe_route_decode_pool call: routing + experts)",
+                     "kernel": _decode_kernel_name(True) + " (one fm_moe_route_decode_pool call: routing + experts)",
                      "kernel_us": fused_ms * 1e3, "bytes_per_launch": fused_bytes,
-                     "decode_only": {"kernel": "fm_decode_cu_kernel<16, false> (one fm_moe_decode_pool call, "
+                     "decode_only": {"kernel": _decode_kernel_name(False) + " (one fm_moe_decode_pool call, "
                                                "routing done by fm_route_kernel)",
                                      "kernel_us": kern_ms * 1e3, "bytes_per_launch": kern_bytes,
                                      "achieved": achieved, "frac": achieved / HBM_PEAK_GBS,
