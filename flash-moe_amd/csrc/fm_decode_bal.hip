@@ -74,12 +74,13 @@ struct FmbUnit {
     fmm_u2 sc, bi;
 };
 
-// 32 MFMAs over 16 groups with the codes already in lane order: v[p][h] holds
-// row n's words 64 p + 16 h + 4 kq .. + 3 (2-bit: p = 0 only).  MASK: lanes
+// 2 NG MFMAs over NG groups with the codes already in lane order: v[p][h]
+// holds row n's words 64 p + 16 h + 4 kq .. + 3 (2-bit, or NG = 8: p = 0 only;
+// 2-bit with NG = 8: h < 2 only).  MASK: lanes
 // with !colok contribute zero codes (their column belongs to the other bit
 // width of a mixed tile).  4-bit: the x quads of the lane's own group are kept
 // in registers and selected per step; 2-bit: read from LDS one step ahead.
-template <int BITS, bool MASK>
+template <int BITS, bool MASK, int NG>  // NG: groups of the unit (16: 32 MFMAs, 8: 16)
 FM_DEV void fmb_mma(const fm_u4 (&v)[2][4], const fm_h2 *xq_grp0, const fm_h2 *zero, fmm_f4 &d0, fmm_f4 &d1,
                     int lane, bool colok) {
     const int m = lane & 15, kq = lane >> 4;
@@ -90,7 +91,7 @@ FM_DEV void fmb_mma(const fm_u4 (&v)[2][4], const fm_h2 *xq_grp0, const fm_h2 *z
         const fmm_h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
         const bool kq_on = (kq >> 1) == (m & 1);
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
+        for (int j = 0; j < 2 * NG; j++) {
             const int p = j >> 4, c = j >> 3, i = j & 7;
             const bool on = kq_on && c == (m >> 2) && (i >> 2) == ((m >> 1) & 1);
             const fmm_h8 xo = on ? xv[i & 3] : z;
@@ -110,10 +111,10 @@ FM_DEV void fmb_mma(const fm_u4 (&v)[2][4], const fm_h2 *xq_grp0, const fm_h2 *z
         };
         fmm_h8 xo = fmm_lds_op(src_of(0));
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
+        for (int j = 0; j < 2 * NG; j++) {
             const int c = j >> 3, i = j & 7;
             fmm_h8 xn = xo;
-            if (j + 1 < 32) xn = fmm_lds_op(src_of(j + 1));
+            if (j + 1 < 2 * NG) xn = fmm_lds_op(src_of(j + 1));
             uint32_t w = fmm_comp(v[0][c], i >> 1);
             if (MASK) w = colok ? w : 0u;
             const fmm_h8 co = fmm_codes<2>(w, i & 1);
@@ -134,33 +135,53 @@ FM_DEV uint64_t fmb_u(const void *p) {
            ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32);
 }
 
-// The loads of gate/up unit (tile of slots sA / sB, input quarter kq4) for
-// intermediate rows 4 c .. 4 c + 3: lane (n, kq) takes tile row n = gate rows
-// of sA (n < 4), up rows of sA, gate rows of sB, up rows of sB (n >= 12).
+// Word offset of load (p, h) of a lane's run in a row's NG-group span (4-bit:
+// 8 words a group, 2-bit: 4): pieces and halves past the span repeat the
+// first ones (cache hits), so the number of loads never depends on the width.
+template <int NG>
+FM_DEV uint32_t fmb_woff(int bits, int p, int h) {
+    if (bits == 4) return (NG == 16 ? 64 * p : 0) + 16 * h;
+    return NG == 16 ? 16 * h : 16 * (h & 1);
+}
+
+// The loads of gate/up unit (tile t, input quarter kq4) for intermediate rows
+// RI c .. RI c + RI - 1 (RI = NG / 4): lane (n, kq) takes tile row n = row
+// n % RI of the gate (up when (n / RI) odd) matrix of tile slot n / (2 RI).
 // Always 8 code loads and 2 scale/bias loads: rows that do not exist or are
-// invalid read `dummy` (cache hits), 2-bit rows repeat piece 0 as piece 1, so
-// the number of loads in flight never depends on a branch.
-FM_DEV void fmb_issue_gu(const FmSlot &A, const FmSlot &B, bool okA, bool okB, uint32_t c, int kq4, FmbUnit &u,
-                         int lane, const void *dummy) {
+// invalid read `dummy`, so the number of loads in flight never depends on a
+// branch.
+template <int NG>
+FM_DEV void fmb_issue_gu(const FmSlot *sl, const bool *ok, uint32_t c, int kq4, FmbUnit &u, int lane,
+                         const void *dummy) {
+    constexpr int RI = NG / 4, SPT = 8 / RI, GH = 4 * NG;
     const int n = lane & 15, kq = lane >> 4;
-    const bool inB = n >= 8, up = (n >> 2) & 1;
-    // per-lane selects of wave-uniform values (made opaque first: selects
-    // of the struct fields themselves became loads through scratch)
-    const bool ok = inB ? okB : okA;
-    const int bits = inB ? fmb_u(B.bits) : fmb_u(A.bits);
-    const uint32_t *W = (const uint32_t *)(inB ? (up ? fmb_u(B.uw) : fmb_u(B.gw)) : (up ? fmb_u(A.uw) : fmb_u(A.gw)));
-    const uint16_t *Sc = (const uint16_t *)(inB ? (up ? fmb_u(B.us) : fmb_u(B.gs)) : (up ? fmb_u(A.us) : fmb_u(A.gs)));
-    const uint16_t *Bi = (const uint16_t *)(inB ? (up ? fmb_u(B.ub) : fmb_u(B.gb)) : (up ? fmb_u(A.ub) : fmb_u(A.gb)));
-    const uint32_t row = 4 * c + (n & 3);
-    const uint32_t wpg = 2 * bits, wpr = FMM_GH * wpg;
-    const uint32_t *base = ok ? W + (size_t)row * wpr + 16 * kq4 * wpg + 4 * kq : (const uint32_t *)dummy + 4 * kq;
+    const int hs = n / (2 * RI);
+    const bool up = (n / RI) & 1;
+    // per-lane selects of wave-uniform values (made opaque first: selects of
+    // the struct fields themselves became loads through scratch)
+    bool okl = false;
+    int bits = 4;
+    uint64_t W = 0, Sc = 0, Bi = 0;
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+        const bool me = hs == j;
+        okl = me ? ok[j] : okl;
+        bits = me ? fmb_u(sl[j].bits) : bits;
+        W = me ? (up ? fmb_u(sl[j].uw) : fmb_u(sl[j].gw)) : W;
+        Sc = me ? (up ? fmb_u(sl[j].us) : fmb_u(sl[j].gs)) : Sc;
+        Bi = me ? (up ? fmb_u(sl[j].ub) : fmb_u(sl[j].gb)) : Bi;
+    }
+    const uint32_t row = RI * c + (n % RI);
+    const uint32_t wpg = 2 * bits, wpr = GH * wpg;
+    const uint32_t *base = okl ? (const uint32_t *)W + (size_t)row * wpr + NG * kq4 * wpg + 4 * kq
+                               : (const uint32_t *)dummy + 4 * kq;
 #pragma unroll
     for (int p = 0; p < 2; p++)
 #pragma unroll
-        for (int h = 0; h < 4; h++) u.v[p][h] = fm_ldg_u4_nt(base + ((ok && bits == 4) ? 64 * p : 0) + 16 * h);
-    const size_t o = (size_t)row * FMM_GH + 16 * kq4 + 4 * kq;
-    u.sc = *(const FM_GLOBAL fmm_u2 *)(ok ? Sc + o : (const uint16_t *)dummy);
-    u.bi = *(const FM_GLOBAL fmm_u2 *)(ok ? Bi + o : (const uint16_t *)dummy);
+        for (int h = 0; h < 4; h++) u.v[p][h] = fm_ldg_u4_nt(base + (okl ? fmb_woff<NG>(bits, p, h) : 16 * h));
+    const size_t o = (size_t)row * GH + NG * kq4 + 4 * (kq & (NG / 4 - 1));
+    u.sc = *(const FM_GLOBAL fmm_u2 *)(okl ? (const uint16_t *)Sc + o : (const uint16_t *)dummy);
+    u.bi = *(const FM_GLOBAL fmm_u2 *)(okl ? (const uint16_t *)Bi + o : (const uint16_t *)dummy);
 }
 
 // One 16-byte run per lane into LDS (lane l's run lands at lds + 16 l) by the
@@ -189,8 +210,10 @@ FM_DEV void fmb_arrive(uint32_t *ctr) {
 // One 64-element group of a vector held 16 values per lane (4 lanes per group,
 // lane qq holds elements 16 qq .. 16 qq + 15) -> operand rows of layout `bits`
 // (4-bit: pairs 8 qq .. 8 qq + 7 of the fmm_build_pair layout; 2-bit: pairs
-// 8 qq .. + 7 of its 2-bit layout), the group's sum and 2^(24 - e).
-FM_DEV void fmb_build_group(const float (&v)[16], int qq, int bits, fm_h2 *dst, float *gsum, float *ginv) {
+// 8 qq .. + 7 of its 2-bit layout), the group's sum and 2^(24 - e).  Lanes
+// with !st compute (the shuffles stay within each lane quad) but store nothing.
+FM_DEV void fmb_build_group(const float (&v)[16], int qq, int bits, fm_h2 *dst, float *gsum, float *ginv,
+                             bool st = true) {
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j++) mx = fmaxf(mx, fabsf(v[j]));
@@ -204,35 +227,42 @@ FM_DEV void fmb_build_group(const float (&v)[16], int qq, int bits, fm_h2 *dst, 
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float m = (j & 1) ? 0.0625f * f : f;
-                dst[4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
+                if (st) dst[4 * (2 * qq + h) + j] = fm_pack_h2(v[8 * h + j] * m, v[8 * h + 4 + j] * m);
             }
     } else {
         const float mt[8] = {1.f, 0.25f, 0.0625f, 0.015625f, 0.00390625f, 1.f, 0.25f, 0.0625f};
 #pragma unroll
-        for (int n2 = 0; n2 < 8; n2++) dst[8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
+        for (int n2 = 0; n2 < 8; n2++)
+            if (st) dst[8 * qq + n2] = fm_pack_h2(v[n2] * (mt[n2] * f), v[8 + n2] * (mt[n2] * f));
     }
     float sm = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j += 4) sm += (v[j] + v[j + 1]) + (v[j + 2] + v[j + 3]);
     sm += __shfl_xor(sm, 1, 64);
     sm += __shfl_xor(sm, 2, 64);
-    if (qq == 0) {
+    if (st && qq == 0) {
         *gsum = sm;
         *ginv = fm_exp2i(24 - ex);
     }
 }
 
+// NG: input groups of a quarter of a gate/up row = hidden / 256 (16: hidden
+// 4096 / inter 1024; 8: hidden 2048 / inter 512).  With inter = hidden / 4,
+// workgroup c owns RI = NG / 4 intermediate rows and RD = NG output rows of
+// every slot, and a 16-row gate/up tile holds SPT = 8 / RI slots' rows.
 // RT: routing fused into the launch (FmDecodeArgs::route_logits).
 // TAG: the activations are handed off as tagged words that each down wave
 // polls (no flag round); otherwise as plain words behind one flag per CU.
-template <bool RT, bool TAG>
+template <int NG, bool RT, bool TAG>
 __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeArgs a) {
     __shared__ FmbLds L;
+    constexpr uint32_t H = 256 * NG, I = 64 * NG, GI = NG;
+    constexpr int RI = NG / 4, RD = NG, SPT = 8 / RI;
+    static_assert(H <= FMM_H && I <= FMM_MAXI, "LDS is sized for hidden 4096 / inter 1024");
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, q = lane >> 4;
-    constexpr uint32_t I = FMM_MAXI;
-    const int S = a.S, NT = (S + 1) >> 1;
+    const int S = a.S, NT = (S + SPT - 1) / SPT;
     const uint32_t c = blockIdx.x;
 
     if (RT && tid < FMC_THREADS / 8) L.rt.ck[tid] = 0;
@@ -246,7 +276,7 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     __syncthreads();
 
     if (wv >= FMB_GU) {
-        // ---- DMA waves: every slot's 16 down rows into LDS, behind the gate/up loads ----
+        // ---- DMA waves: every slot's RD down rows into LDS, behind the gate/up loads ----
         float winv = 1.f;
         if constexpr (RT) {
             fmc_route_bystander(L);
@@ -256,20 +286,23 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         }
         const int *rsel = RT ? L.rsel : nullptr;
         if (FMB_DN_AFTER_GU) fmb_wait_lds(a, &L.gu_issued, FMB_GU);
+        // scale / bias runs of the tile: RD rows x GI groups x 2 B each, 16 B a lane
+        constexpr int NSC = RD * GI * 2 / 16;
         for (int sd = wv - FMB_GU; sd < S; sd += FMB_W - FMB_GU) {
             const FmSlot sD = fmc_slot(a, sd, rsel, L.rp, winv);
             const bool okD = sD.valid;
-            const uint32_t wpr = FMM_GI * 2 * sD.bits;
+            const uint32_t wpr = GI * 2 * sD.bits;
             const uint32_t *base =
-                okD ? sD.dw + (size_t)(16 * c + n) * wpr + 4 * q : (const uint32_t *)a.x + 4 * q;
+                okD ? sD.dw + (size_t)(RD * c + n % RD) * wpr + 4 * q : (const uint32_t *)a.x + 4 * q;
 #pragma unroll
             for (int p = 0; p < 2; p++)
 #pragma unroll
                 for (int h = 0; h < 4; h++)
-                    fmb_dma16(&L.dn[sd][p][h][0], base + ((okD && sD.bits == 4) ? 64 * p : 0) + 16 * h);
-            const uint16_t *sb = lane < 32 ? sD.ds : sD.db;
-            fmb_dma16(&L.dsb[sd][0][0],
-                      okD ? sb + (size_t)16 * c * FMM_GI + 8 * (lane & 31) : (const uint16_t *)a.x);
+                    fmb_dma16(&L.dn[sd][p][h][0], base + (okD ? fmb_woff<NG>(sD.bits, p, h) : 16 * h));
+            const bool lsc = lane < 2 * NSC;
+            const uint16_t *sb = lane < NSC ? sD.ds : sD.db;
+            fmb_dma16(&L.dsb[sd][0][0], (okD && lsc) ? sb + (size_t)RD * c * GI + 8 * (lane % NSC)
+                                                      : (const uint16_t *)a.x);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies have landed
         fmb_arrive(&L.dn_ready);
@@ -286,10 +319,11 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         for (int j = 0; j < FMC_THREADS / 64; j++)
             lgq[j] = 64 * j + lane < a.route_E ? a.route_logits[64 * j + lane] : -INFINITY;
     }
-    // x: waves 0-3, 16 elements a thread (thread t: elements 16 t .. 16 t + 15)
+    // x: the first H / 1024 waves, 16 elements a thread (thread t: elements 16 t .. 16 t + 15)
+    constexpr int XT = (int)H / 16, XW = XT / 64;
     fm_f4 xr[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (tid < 256 ? tid : 0) + 4 * j);
+    for (int j = 0; j < 4; j++) xr[j] = fm_ldg_f4(a.x + 16 * (tid < XT ? tid : 0) + 4 * j);
     // the shared expert's gate input, loaded before the weight stream so that
     // reading it waits for nothing else
     const float sscore = (wv == 0 && a.shared_score) ? a.shared_score[0] : 0.f;
@@ -298,17 +332,21 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     const int *rsel = RT ? L.rsel : nullptr;
 
     // gate/up units: wave w takes units w and w + 12 (unit u = tile u / 4, input quarter u % 4)
-    const int t0 = wv >> 2, t1 = FMB_TILES / 2 + (wv >> 2), kq4 = wv & 3;
+    const int t0 = wv >> 2, t1 = FMB_GU / 4 + (wv >> 2), kq4 = wv & 3;
     const bool has0 = t0 < NT, has1 = t1 < NT;
-    const FmSlot sA0 = fmc_slot(a, has0 ? 2 * t0 : 0, rsel, L.rp, winv);
-    const FmSlot sB0 = fmc_slot(a, (has0 && 2 * t0 + 1 < S) ? 2 * t0 + 1 : 0, rsel, L.rp, winv);
-    const FmSlot sA1 = fmc_slot(a, has1 ? 2 * t1 : 0, rsel, L.rp, winv);
-    const FmSlot sB1 = fmc_slot(a, (has1 && 2 * t1 + 1 < S) ? 2 * t1 + 1 : 0, rsel, L.rp, winv);
-    const bool okA0 = has0 && sA0.valid, okB0 = has0 && 2 * t0 + 1 < S && sB0.valid;
-    const bool okA1 = has1 && sA1.valid, okB1 = has1 && 2 * t1 + 1 < S && sB1.valid;
+    FmSlot s0[SPT], s1[SPT];
+    bool ok0[SPT], ok1[SPT];
+#pragma unroll
+    for (int j = 0; j < SPT; j++) {
+        const int k0 = SPT * t0 + j, k1 = SPT * t1 + j;
+        s0[j] = fmc_slot(a, has0 && k0 < S ? k0 : 0, rsel, L.rp, winv);
+        s1[j] = fmc_slot(a, has1 && k1 < S ? k1 : 0, rsel, L.rp, winv);
+        ok0[j] = has0 && k0 < S && s0[j].valid;
+        ok1[j] = has1 && k1 < S && s1[j].valid;
+    }
     FmbUnit u0, u1;
-    fmb_issue_gu(sA0, sB0, okA0, okB0, c, kq4, u0, lane, a.x);
-    fmb_issue_gu(sA1, sB1, okA1, okB1, c, kq4, u1, lane, a.x);
+    fmb_issue_gu<NG>(s0, ok0, c, kq4, u0, lane, a.x);
+    fmb_issue_gu<NG>(s1, ok1, c, kq4, u1, lane, a.x);
     if (FMB_DN_AFTER_GU) fmb_arrive(&L.gu_issued);
     // this wave's down slot (waves 0 .. S - 1)
     const int sd = wv;
@@ -331,8 +369,8 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
             L.sw = (a.has_shared || a.shared_y) ? (a.shared_score ? fm_sigmoid(sscore) : a.shared_w_host) : 0.f;
         }
     }
-    // x -> operand rows (both layouts), group sums and scales: waves 0-3
-    if (wv < 4) {
+    // x -> operand rows (both layouts), group sums and scales: the first XW waves
+    if (wv < XW) {
         if (tid < 32) L.zero[tid] = fm_as_h2(0u);
         const int g = tid >> 2, qq = tid & 3;
         float v[16];
@@ -348,33 +386,47 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         fmb_build_group(v, qq, 2, &L.xq[1][g][0], &unused_s, &unused_i);
         fmb_arrive(&L.xready);
     }
-    fmb_wait_lds(a, &L.xready, 4);
+    fmb_wait_lds(a, &L.xready, XW);
     const uint32_t ep = fm_epoch_tag(ep_ld);
 
     // ---- gate/up MMAs of the two units ----
-    // bit width of each half of a tile (an invalid half takes the other's, so
-    // only a tile of two valid slots of different widths needs two passes)
-    const int bA0 = okA0 ? sA0.bits : (okB0 ? sB0.bits : 4), bB0 = okB0 ? sB0.bits : bA0;
-    const int bA1 = okA1 ? sA1.bits : (okB1 ? sB1.bits : 4), bB1 = okB1 ? sB1.bits : bA1;
-    auto unit_mma = [&](const FmbUnit &u, int bA, int bB, int t) __attribute__((always_inline)) {
-        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
-        const fm_h2 *x4 = &L.xq[0][16 * kq4][0], *x2 = &L.xq[1][16 * kq4][0];
-        if (bA == bB) {
-            if (bA == 4)
-                fmb_mma<4, false>(u.v, x4, L.zero, d0, d1, lane, true);
-            else
-                fmb_mma<2, false>(u.v, x2, L.zero, d0, d1, lane, true);
-        } else {
-            const bool col4 = (n < 8 ? bA : bB) == 4;
-            fmb_mma<4, true>(u.v, x4, L.zero, d0, d1, lane, col4);
-            fmb_mma<2, true>(u.v, x2, L.zero, d0, d1, lane, !col4);
+    // the widths present in a tile (invalid rows take any: their sums are
+    // never used); a tile of both widths runs both MMAs with the other
+    // width's columns masked
+    auto tile_bits = [&](const FmSlot *sl, const bool *ok, bool &w4, bool &w2) __attribute__((always_inline)) {
+        w4 = w2 = false;
+#pragma unroll
+        for (int j = 0; j < SPT; j++) {
+            w4 |= ok[j] && sl[j].bits == 4;
+            w2 |= ok[j] && sl[j].bits == 2;
         }
-        float p = fmm_fold(d0 + d1, u.sc, u.bi, &L.xsum[16 * kq4 + 4 * q], &L.xinv[16 * kq4 + 4 * q]);
+    };
+    auto unit_mma = [&](const FmbUnit &u, const FmSlot *sl, const bool *ok, int t) __attribute__((always_inline)) {
+        bool w4, w2;
+        tile_bits(sl, ok, w4, w2);
+        fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
+        const fm_h2 *x4 = &L.xq[0][NG * kq4][0], *x2 = &L.xq[1][NG * kq4][0];
+        if (!(w4 && w2)) {
+            if (!w2)
+                fmb_mma<4, false, NG>(u.v, x4, L.zero, d0, d1, lane, true);
+            else
+                fmb_mma<2, false, NG>(u.v, x2, L.zero, d0, d1, lane, true);
+        } else {
+            int rb = 4;
+#pragma unroll
+            for (int j = 0; j < SPT; j++) rb = n / (2 * RI) == j ? sl[j].bits : rb;
+            const bool col4 = rb == 4;
+            fmb_mma<4, true, NG>(u.v, x4, L.zero, d0, d1, lane, col4);
+            fmb_mma<2, true, NG>(u.v, x2, L.zero, d0, d1, lane, !col4);
+        }
+        const bool qok = 4 * q < NG;
+        const int gq = NG * kq4 + 4 * (qok ? q : 0);
+        float p = qok ? fmm_fold(d0 + d1, u.sc, u.bi, &L.xsum[gq], &L.xinv[gq]) : 0.f;
         p = fmm_q_sum(p);
         if (lane < 16) L.part[t][kq4][n] = p;
     };
-    if (has0) unit_mma(u0, bA0, bB0, t0);
-    if (has1) unit_mma(u1, bA1, bB1, t1);
+    if (has0) unit_mma(u0, s0, ok0, t0);
+    if (has1) unit_mma(u1, s1, ok1, t1);
     fmb_arrive(&L.pdone);
     if (RT && wv == FMB_GU - 1 && c == gridDim.x - 1) {
         // cpu_topk's slot order by serial replay, then cpu_normalize_weights
@@ -394,19 +446,19 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         }
     }
 
-    // ---- wave 0: SwiGLU of the CU's 4 S activations, publish, then wait for every CU ----
+    // ---- wave 0: SwiGLU of the CU's RI S activations, publish, then wait for every CU ----
+    // activation i of a slot is stored at (I / 16) (i % 16) + i / 16: a reader
+    // lane l < I / 16 then holds elements 16 l .. 16 l + 15 with 16 coalesced loads
     float *actf = a.actf;
     if (wv == 0) {
         fmb_wait_lds(a, &L.pdone, FMB_GU);
         if (lane < 8 * NT) {
-            const int t = lane >> 3, r8 = lane & 7, s = 2 * t + (r8 >> 2), rr = r8 & 3;
-            const int ng = (r8 >> 2) * 8 + rr, nu = ng + 4;
+            const int t = lane >> 3, r8 = lane & 7, hs = r8 / RI, rr = r8 % RI, s = SPT * t + hs;
+            const int ng = hs * 2 * RI + rr, nu = ng + RI;
             const float g = (L.part[t][0][ng] + L.part[t][1][ng]) + (L.part[t][2][ng] + L.part[t][3][ng]);
             const float u = (L.part[t][0][nu] + L.part[t][1][nu]) + (L.part[t][2][nu] + L.part[t][3][nu]);
-            const uint32_t i = 4 * c + rr;
-            // stored at 64 (i % 16) + i / 16: a reader lane l then holds
-            // elements 16 l .. 16 l + 15 with 16 fully coalesced loads
-            const size_t pos = (size_t)s * I + 64 * (i & 15) + (i >> 4);
+            const uint32_t i = RI * c + rr;
+            const size_t pos = (size_t)s * I + (I / 16) * (i & 15) + (i >> 4);
             if (s < S) {
                 if (TAG)
                     fm_put_tagged(&a.act2[pos], fm_silu_mul(g, u), ep);
@@ -440,15 +492,17 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         if (c == 0 && lane == 0) fm_epoch_publish(a, ep);
     }
 
-    // ---- down: the slot's activations -> operand rows, 16 down rows from LDS ----
+    // ---- down: the slot's activations -> operand rows, RD down rows from LDS ----
     if (down) {
+        constexpr int AL = (int)I / 16;  // lanes holding activations
+        const bool al = lane < AL;
         float v[16];
         if constexpr (TAG) {
-            // the slot's 1024 tagged activations (every CU stored 4 of them)
-            const uint64_t *src = a.act2 + (size_t)sd * I + lane;
+            // the slot's I tagged activations (every CU stored RI of them)
+            const uint64_t *src = a.act2 + (size_t)sd * I + (al ? lane : 0);
             uint64_t t[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) t[i] = fm_get_tagged(src + 64 * i);
+            for (int i = 0; i < 16; i++) t[i] = fm_get_tagged(src + AL * i);
             uint32_t it = 0;
             do {
                 bool ready = true;
@@ -457,7 +511,7 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
                 if (__all(ready)) break;
 #pragma unroll
                 for (int i = 0; i < 16; i++)
-                    if ((uint32_t)(t[i] >> 32) != ep) t[i] = fm_get_tagged(src + 64 * i);
+                    if ((uint32_t)(t[i] >> 32) != ep) t[i] = fm_get_tagged(src + AL * i);
             } while (++it < FM_SPIN_MAX);
             if (it >= FM_SPIN_MAX && lane == 0) atomicOr(a.err, FM_STATUS_WAIT_TIMEOUT);
 #pragma unroll
@@ -469,13 +523,14 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
             fmb_wait_lds(a, &L.go, 1);
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                v[i] = __hip_atomic_load(&actf[(size_t)sd * I + 64 * i + lane], __ATOMIC_RELAXED,
+                v[i] = __hip_atomic_load(&actf[(size_t)sd * I + AL * i + (al ? lane : 0)], __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
         }
         float y = 0.f;
         if (okD) {
-            fmb_build_group(v, lane & 3, sD.bits, &L.aq[sd][lane >> 2][0], &L.asum[sd][lane >> 2],
-                            &L.ainv[sd][lane >> 2]);
+            // lanes l < I / 16: group l / 4, elements 16 (l % 4) .. + 15
+            const int g = al ? lane >> 2 : 0;
+            fmb_build_group(v, lane & 3, sD.bits, &L.aq[sd][g][0], &L.asum[sd][g], &L.ainv[sd][g], al);
             fm_wave_lds_sync();
             fmb_wait_lds(a, &L.dn_ready, FMB_W - FMB_GU);
             fm_u4 dv[2][4];
@@ -485,28 +540,32 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
                 for (int h = 0; h < 4; h++) dv[p][h] = L.dn[sd][p][h][lane];
             fmm_f4 d0 = {0, 0, 0, 0}, d1 = d0;
             if (sD.bits == 4)
-                fmb_mma<4, false>(dv, &L.aq[sd][0][0], L.zero, d0, d1, lane, true);
+                fmb_mma<4, false, NG>(dv, &L.aq[sd][0][0], L.zero, d0, d1, lane, true);
             else
-                fmb_mma<2, false>(dv, &L.aq[sd][0][0], L.zero, d0, d1, lane, true);
-            const fmm_u2 sc = *(const fmm_u2 *)&L.dsb[sd][0][16 * n + 4 * q];
-            const fmm_u2 bi = *(const fmm_u2 *)&L.dsb[sd][1][16 * n + 4 * q];
-            y = fmm_q_sum(fmm_fold(d0 + d1, sc, bi, &L.asum[sd][4 * q], &L.ainv[sd][4 * q]));
+                fmb_mma<2, false, NG>(dv, &L.aq[sd][0][0], L.zero, d0, d1, lane, true);
+            const bool qok = 4 * q < NG;
+            const uint16_t *sbl = &L.dsb[sd][0][0];
+            const int o = GI * (n % RD) + 4 * (qok ? q : 0);
+            const fmm_u2 sc = *(const fmm_u2 *)&sbl[o];
+            const fmm_u2 bi = *(const fmm_u2 *)&sbl[RD * GI + o];
+            y = qok ? fmm_fold(d0 + d1, sc, bi, &L.asum[sd][4 * (qok ? q : 0)], &L.ainv[sd][4 * (qok ? q : 0)]) : 0.f;
+            y = fmm_q_sum(y);
         }
-        if (lane < 16) {
+        if (lane < RD) {
             if (a.mode == 1)
-                a.expert_out[(size_t)sd * FMM_H + 16 * c + n] = y;
+                a.expert_out[(size_t)sd * H + RD * c + n] = y;
             else
                 L.y[sd][n] = y;
         }
         fmb_arrive(&L.ydone);
     }
 
-    // ---- wave 0: the combine of the CU's 16 rows over every slot, in slot order ----
+    // ---- wave 0: the combine of the CU's RD rows over every slot, in slot order ----
     if (wv == 0 && a.mode == 0) {
         fmb_wait_lds(a, &L.ydone, (uint32_t)S);
-        const uint32_t row = 16 * c + n;
+        const uint32_t row = RD * c + (n % RD);
         float o = 0.f;
-        if (lane < 16) {
+        if (lane < RD) {
             const uint32_t cv = L.cvalid;
             float moe = 0.f;
 #pragma unroll
@@ -522,9 +581,9 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
         }
         if (a.norm_w) {
             // next layer's input RMS norm (cpu_kernels.h:235-246): every CU
-            // publishes the sum of squares of its 16 rows (tagged), then every
+            // publishes the sum of squares of its RD rows (tagged), then every
             // CU adds all of them in the same fixed order (all 64 lanes here)
-            const float sq = fm_lane_sum<16>(lane < 16 ? o * o : 0.f);
+            const float sq = fm_lane_sum<16>(lane < RD ? o * o : 0.f);
             const uint32_t G = gridDim.x;
             uint64_t *ssq = a.flags + G;
             if (lane == 0) fm_put_tagged(&ssq[c], sq, ep);
@@ -547,8 +606,8 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
 #pragma unroll
             for (int j = 0; j < 4; j++) part += 64 * j + lane < (int)G ? __uint_as_float((uint32_t)t[j]) : 0.f;
             const float tot = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fm_lane_sum<64>(part))));
-            const float inv = 1.0f / sqrtf(tot / (float)FMM_H + a.norm_eps);
-            if (lane < 16) a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
+            const float inv = 1.0f / sqrtf(tot / (float)H + a.norm_eps);
+            if (lane < RD) a.normed[row] = o * inv * fm_bf16_to_f32(a.norm_w[row]);
         }
     }
     if (a.pool_mode && !RT && c == 0 && tid < a.K) {
@@ -557,35 +616,43 @@ __global__ __launch_bounds__(FMB_THREADS, 1) void fm_decode_bal_kernel(FmDecodeA
     }
 }
 
-// hidden 4096 / inter 1024, 1 .. 11 slots a token, no fused norm with several
-// tokens: one workgroup per CU for the 256 row blocks (every one must be
-// resident: each waits for all the others' activations).  Several tokens (pool
-// mode, the combine) run as one launch per token on the same workspace (each
-// launch tags with its own epoch).
+// hidden 4096 / inter 1024 or hidden 2048 / inter 512, 1 .. 11 slots a token:
+// one workgroup per CU for the 256 row blocks (every one must be resident:
+// each waits for all the others' activations).  Several tokens (pool mode, the
+// combine, no fused norm) run as one launch per token on the same workspace
+// (each launch tags with its own epoch).
+template <int NG>
+static void (*fmb_kernel(bool rt, bool tagged))(FmDecodeArgs) {
+    return rt ? (tagged ? fm_decode_bal_kernel<NG, true, true> : fm_decode_bal_kernel<NG, true, false>)
+              : (tagged ? fm_decode_bal_kernel<NG, false, true> : fm_decode_bal_kernel<NG, false, false>);
+}
+
 int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
     // opt-in (FMOE_DECODE_BAL=1) until it has been measured on the GPU;
     // FMOE_DECODE_NO_BAL set: off
     const char *on = getenv("FMOE_DECODE_BAL"), *off = getenv("FMOE_DECODE_NO_BAL");
     if (!(on && *on == '1') || (off && *off)) return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: disabled");
     const int ntok = a.ntok > 1 ? a.ntok : 1, spt = ntok > 1 ? a.spt : a.S;
-    if (a.hidden != FMM_H || a.inter != FMM_MAXI || spt < 1 || spt > FMB_MAXS || (a.norm_w && a.mode != 0) ||
-        !a.actf || !a.flags)
+    const int ng = a.hidden == 4096 && a.inter == 1024 ? 16 : (a.hidden == 2048 && a.inter == 512 ? 8 : 0);
+    if (!ng || spt < 1 || spt > FMB_MAXS || (a.norm_w && a.mode != 0) || !a.actf || !a.flags)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: shape");
     if (ntok > 1 && (!a.pool_mode || a.mode != 0 || a.norm_w || a.route_logits || a.S != ntok * spt))
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: several tokens need pool mode and the combine");
     if (a.route_logits && !(a.mode == 0 && a.pool_mode && a.K >= 1 && a.K <= 64 && a.route_E >= a.K &&
                             a.route_E <= FMC_THREADS))
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: fused routing");
-    const uint32_t grid = FMM_H / 16;
+    const uint32_t grid = 256;  // hidden / (output rows of a workgroup)
     static int per_cu = -1;
     if (per_cu < 0 &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_bal_kernel<false, false>, FMB_THREADS, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fm_decode_bal_kernel<16, false, false>, FMB_THREADS,
+                                                     0) != hipSuccess)
         per_cu = 0;
     if (per_cu < 1 || (uint32_t)(per_cu * fm_num_cus()) < grid)
         return fm_fail(FM_ERR_UNSUPPORTED, "bal decode: %u workgroups not resident", grid);
     // FMOE_BAL_TAGGED=1: the tagged-activation hand-off (measured against the flag round)
     const char *tg = getenv("FMOE_BAL_TAGGED");
     const bool tagged = tg && *tg == '1';
+    const size_t H = a.hidden;
     for (int t = 0; t < ntok; t++) {
         FmDecodeArgs b = a;
         if (ntok > 1) {
@@ -593,15 +660,13 @@ int fm_launch_decode_bal(FmDecodeArgs &a, hipStream_t st) {
             b.spt = b.S = spt;
             b.idx = a.idx + (size_t)t * a.K;
             b.wdev = a.wdev + (size_t)t * a.K;
-            b.x = a.x + (size_t)t * FMM_H;
-            b.out = a.out + (size_t)t * FMM_H;
-            if (a.h_mid) b.h_mid = a.h_mid + (size_t)t * FMM_H;
-            if (a.out_bf16) b.out_bf16 = a.out_bf16 + (size_t)t * FMM_H;
+            b.x = a.x + (size_t)t * H;
+            b.out = a.out + (size_t)t * H;
+            if (a.h_mid) b.h_mid = a.h_mid + (size_t)t * H;
+            if (a.out_bf16) b.out_bf16 = a.out_bf16 + (size_t)t * H;
             if (a.shared_score) b.shared_score = a.shared_score + t;
         }
-        void (*kern)(FmDecodeArgs) =
-            b.route_logits ? (tagged ? fm_decode_bal_kernel<true, true> : fm_decode_bal_kernel<true, false>)
-                           : (tagged ? fm_decode_bal_kernel<false, true> : fm_decode_bal_kernel<false, false>);
+        void (*kern)(FmDecodeArgs) = ng == 16 ? fmb_kernel<16>(b.route_logits, tagged) : fmb_kernel<8>(b.route_logits, tagged);
         hipLaunchKernelGGL(kern, dim3(grid), dim3(FMB_THREADS), 0, st, b);
         const int rc = fm_check_launch("fm_decode_bal_kernel");
         if (rc) return rc;

@@ -1851,6 +1851,12 @@ static bool fmc_route_fits(const FmDecodeArgs &a, uint32_t tiles, int cus) {
 
 int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
     if (a.norm_w && a.mode != 0) return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: norm needs the combine");
+    // up to 11 slots a token: the row-split kernel where it is enabled
+    {
+        const int rc = fm_launch_decode_bal(a, st);
+        if (rc != FM_ERR_UNSUPPORTED) return rc;
+        fm_clear_error();
+    }
     const int cus = fm_num_cus();
     if (a.route_logits && !fmc_route_fits(a, a.hidden / 64, cus))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: fused routing does not fit this launch");
@@ -1887,12 +1893,6 @@ int fm_launch_decode_mfma(FmDecodeArgs &a, hipStream_t st) {
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: %d slots", a.S);
     if (a.ntok > 1 && (a.norm_w || a.mode != 0 || !a.pool_mode))
         return fm_fail(FM_ERR_UNSUPPORTED, "mfma decode: several tokens need pool mode and the combine");
-    // up to 11 slots a token: the row-split kernel where it is enabled
-    {
-        const int rc = fm_launch_decode_bal(a, st);
-        if (rc != FM_ERR_UNSUPPORTED) return rc;
-        fm_clear_error();
-    }
     // up to four slots of one token (no fused norm): the split kernel
     if (a.ntok <= 1 && a.S <= FMS_MAXS && !a.norm_w && !a.route_logits) {
         const char *no_split = getenv("FMOE_DECODE_NO_SPLIT");

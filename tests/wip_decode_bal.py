@@ -42,11 +42,12 @@ def _bits(mode, n):
     return [4 if i % 3 else 2 for i in range(n)]  # mixed: tiles of two widths
 
 
-def _step(orc, dev, K, mode, shared, seed, monkeypatch, valid=None):
+def _step(orc, dev, K, mode, shared, seed, monkeypatch, valid=None, hidden=HIDDEN, inter=INTER):
     import torch
+    HIDDEN, INTER = hidden, inter  # noqa: N806 (the step's shape)
     n = K + (1 if shared else 0)
     bl = _bits(mode, n)
-    blobs = experts(range(9100 + 20 * seed, 9100 + 20 * seed + n), bl)
+    blobs = experts(range(9100 + 20 * seed, 9100 + 20 * seed + n), bl, HIDDEN, INTER)
     rng = synth.rng_for(91, K, seed, sum(map(ord, mode)))
     x = synth.hidden_vec(rng, HIDDEN)
     hm = rng.normal(0, 1, HIDDEN).astype(np.float32)
@@ -86,6 +87,15 @@ def _step(orc, dev, K, mode, shared, seed, monkeypatch, valid=None):
 def test_bal_step(orc, dev, monkeypatch, K, shared, mode):
     say("bal decode", K, shared, mode)
     _step(orc, dev, K, mode, shared, 0, monkeypatch)
+
+
+@pytest.mark.parametrize("mode", ["4", "mixed"])
+@pytest.mark.parametrize("K,shared", [(8, True), (5, False), (11, False)])
+def test_bal_step_2048(orc, dev, monkeypatch, K, shared, mode):
+    """The hidden 2048 / inter 512 shape (Qwen3.5-35B-A3B experts): 2
+    intermediate and 8 output rows of every slot per CU, 4 slots a gate/up tile."""
+    say("bal decode 2048/512", K, shared, mode)
+    _step(orc, dev, K, mode, shared, 2, monkeypatch, hidden=2048, inter=512)
 
 
 def test_bal_invalid_slots(orc, dev, monkeypatch):
